@@ -1,0 +1,514 @@
+// Grouped bf16 Newton-Schulz / Polar Express chain on CDNA4 MFMA.
+//
+// Replaces the torch.compile'd GEMM chains of
+//   zeropower_via_newtonschulz5   defmuon/optim/muon.py:16-44
+//   PolarExpress                  defmuon/optim/polar_express.py:21-34
+//   _horner_iterate               defmuon/optim/deflation_batched.py:196-211
+// for a batch of same-shape matrices in one launch per GEMM phase.
+//
+// Layout.  Every matrix of the batch is held twice in a zero-padded workspace,
+// as W (m x n, the wide convention, m <= n) and as T = W^T (n x m), both bf16
+// row-major with m, n rounded up to the 256 tile.  One iteration (a, b, c) is
+//
+//   K1  A  = W W^T                  (m x m, K = n)  symmetric: upper tiles only
+//   K2  B  = b A + c A A            (m x m, K = m)  symmetric: upper tiles only
+//   K3  T' = a T + T B ; W' = T'^T  (n x m, K = m)
+//
+// so every product is an "NT" GEMM C[i][j] = sum_k P[i][k] Q[j][k] whose two
+// operands are both K-contiguous, which is the layout the MFMA operand
+// registers want (A and B symmetric make A A and T B NT products).  Zero
+// padding is a fixed point of every phase, so no kernel needs bounds checks on
+// its loads.
+//
+// Rounding follows the reference's compiled graph for batched operands: A is
+// stored bf16; B = bf16(b*A + bf16(c*AA)); T' = bf16(a*T + bf16(TB)).  (The
+// reference rounds c*A to bf16 before the product; this kernel scales the fp32
+// accumulator instead, which keeps A*A symmetric and lets K2 skip half its
+// tiles.)
+#include "common.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+namespace dmh {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM tile: 256 x 256 output per workgroup, 4 waves of 128 x 128, K step 64.
+//
+// Operand tiles go global -> LDS with the gfx950 direct-to-LDS load
+// (global_load_lds_dwordx4: lane L of a wave writes 16 bytes at base + 16 L, no
+// VGPR round trip), two stages.  An LDS row is 64 bf16 = 128 B = 8 chunks of
+// 16 B; chunk c of row r sits in slot c ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1),
+// which makes the 16-byte fragment reads of 8 (or 16) consecutive rows hit
+// distinct banks.  The swizzle is applied by choosing, for each lane, which
+// global chunk it fetches into its fixed LDS slot.
+// ---------------------------------------------------------------------------
+constexpr int TILE = 256;
+constexpr int TK = 64;
+constexpr int ROWB = TK * 2;                 // bytes per LDS row
+constexpr int OPB = TILE * ROWB;             // bytes per operand tile (32 KB)
+constexpr int GEMM_THREADS = 256;
+
+enum { EPI_STORE = 0, EPI_POLY = 1, EPI_AXPY = 2 };
+
+struct GemmArgs {
+  const bf16* P; long long p_bs; int p_ld;      // rows i of C
+  const bf16* Q; long long q_bs; int q_ld;      // rows j of C
+  int K;                                         // multiple of TK
+  int tiles_m, tiles_n;                          // tiles per matrix
+  int sym;                                       // upper-triangular tiles, mirrored stores
+  float alpha, beta;                             // POLY: (b, c); AXPY: (a, -)
+  const bf16* aux; long long aux_bs; int aux_ld; // POLY: A; AXPY: T  (indexed [i][j])
+  bf16* out; long long out_bs; int out_ld;       // C[i][j]   (may be null)
+  bf16* outT; long long outT_bs; int outT_ld;    // C[j][i]   (may be null)
+  int valid_i, valid_j;                          // stores limited to i < valid_i, j < valid_j
+};
+
+__device__ __forceinline__ void decode_tile(const GemmArgs& g, int lid, int& b, int& ti, int& tj) {
+  if (g.sym) {
+    const int T = g.tiles_m;
+    const int per = T * (T + 1) / 2;
+    b = lid / per;
+    int rem = lid - b * per;
+    ti = 0;
+    while (rem >= T - ti) { rem -= T - ti; ++ti; }
+    tj = ti + rem;
+  } else {
+    const int per = g.tiles_m * g.tiles_n;
+    b = lid / per;
+    const int t = lid - b * per;
+    ti = t / g.tiles_n;
+    tj = t - ti * g.tiles_n;
+  }
+}
+
+__device__ __forceinline__ int lds_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int EPI>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_nt_bf16(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * OPB];   // [stage][operand]
+
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  int b, ti, tj;
+  decode_tile(g, lid, b, ti, tj);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const bf16* P = g.P + (long long)b * g.p_bs + (long long)(ti * TILE) * g.p_ld;
+  const bf16* Q = g.Q + (long long)b * g.q_bs + (long long)(tj * TILE) * g.q_ld;
+
+  // Loader: wave w, instruction q covers tile rows 64w + 8q .. +7; lane L fills
+  // slot L & 7 of row 64w + 8q + (L >> 3) with the global chunk slot ^ swz(row).
+  const int lrow0 = 64 * wave + (lane >> 3);
+  const int lslot = lane & 7;
+  int goffP[8], goffQ[8];   // element offsets within the tile (32-bit)
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int r = lrow0 + 8 * q;
+    const int c = lslot ^ lds_swz(r);
+    goffP[q] = r * g.p_ld + c * 8;
+    goffQ[q] = r * g.q_ld + c * 8;
+  }
+  char* const lds_wave = smem + wave * 64 * ROWB;   // this wave's first row in each tile
+
+#define DMH_GLOAD(k0, st)                                                              \
+  do {                                                                                 \
+    char* dP = lds_wave + (st) * 2 * OPB;                                              \
+    char* dQ = dP + OPB;                                                               \
+    _Pragma("unroll") for (int q = 0; q < 8; ++q) {                                    \
+      __builtin_amdgcn_global_load_lds((const void*)(P + (k0) + goffP[q]),             \
+                                       (lds_ptr_t)(dP + q * 8 * ROWB), 16, 0, 0);      \
+      __builtin_amdgcn_global_load_lds((const void*)(Q + (k0) + goffQ[q]),             \
+                                       (lds_ptr_t)(dQ + q * 8 * ROWB), 16, 0, 0);      \
+    }                                                                                  \
+  } while (0)
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int r32 = lane & 31;
+  const int hi = lane >> 5;
+  const int sw = lds_swz(r32);
+  // byte offsets of this lane's fragment rows (row 32i + r32 of the wave's half)
+  const int fP = (128 * wm + r32) * ROWB;
+  const int fQ = OPB + (128 * wn + r32) * ROWB;
+  int fchunk[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) fchunk[s] = ((2 * s + hi) ^ sw) * 16;
+
+  const int nk = g.K / TK;
+  DMH_GLOAD(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+    if (kt + 1 < nk) DMH_GLOAD((kt + 1) * TK, st ^ 1);
+    const char* base = smem + st * 2 * OPB;
+    bf16x8 pf[2][4], qf[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pf[0][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fchunk[0]);
+      qf[0][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fchunk[0]);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pf[cur ^ 1][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fchunk[s + 1]);
+          qf[cur ^ 1][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fchunk[s + 1]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[cur][j], pf[cur][i], acc[i][j],
+                                                              0, 0, 0);
+    }
+    // Schedule: next-stage loads first, the first fragments, then each k16
+    // step's 16 MFMAs with the 8 fragment reads of the next step issued early.
+    __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);   // VMEM (direct-to-LDS loads)
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS read: step-0 fragments
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+#undef DMH_GLOAD
+
+  // ---- epilogue -------------------------------------------------------------
+  // acc[i][j][4g+q] holds C[i0 + (lane&31)][j0 + 8g + 4(lane>>5) + q]
+  const bool diag = g.sym && ti == tj;
+  const bool mirror = g.sym && ti != tj;
+#pragma unroll
+  for (int bi = 0; bi < 4; ++bi) {
+    const int i = ti * TILE + 128 * wm + 32 * bi + r32;
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int j0 = tj * TILE + 128 * wn + 32 * bj + 8 * gq + 4 * (lane >> 5);
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = acc[bi][bj][4 * gq + q];
+        bf16 o[4];
+        if (EPI == EPI_STORE) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = f2bf(v[q]);
+        } else {
+          const bf16* ap = g.aux + (long long)b * g.aux_bs + (long long)i * g.aux_ld + j0;
+          const bf16x4 av = *(const bf16x4*)ap;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (EPI == EPI_POLY)
+              o[q] = f2bf(g.alpha * bf2f(av[q]) + bf2f(f2bf(g.beta * v[q])));
+            else
+              o[q] = f2bf(g.alpha * bf2f(av[q]) + bf2f(f2bf(v[q])));
+          }
+        }
+        if (i >= g.valid_i) continue;
+        if (g.out) {
+          bf16* op = g.out + (long long)b * g.out_bs + (long long)i * g.out_ld + j0;
+          if (!diag && j0 + 3 < g.valid_j && (g.out_ld & 3) == 0) {
+            bf16x4 ov = {o[0], o[1], o[2], o[3]};
+            *(bf16x4*)op = ov;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (j0 + q < g.valid_j && (!diag || i <= j0 + q)) op[q] = o[q];
+          }
+        }
+        if (g.outT && (mirror || diag || !g.sym)) {
+          bf16* tp = g.outT + (long long)b * g.outT_bs + i;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int j = j0 + q;
+            if (j < g.valid_j && (!diag || i < j)) tp[(long long)j * g.outT_ld] = o[q];
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// entry: Frobenius norm partials, then scale + cast + pack into padded T and W
+// ---------------------------------------------------------------------------
+constexpr int NORM_CHUNKS = 64;
+
+struct InView {
+  const void* x; int dtype;            // 0 fp32, 1 bf16
+  long long bs, rs, cs;                // element strides
+  int rows, cols;
+};
+
+__device__ __forceinline__ float load_in(const InView& v, int b, int r, int c) {
+  const long long off = (long long)b * v.bs + (long long)r * v.rs + (long long)c * v.cs;
+  if (v.dtype == 0) return ((const float*)v.x)[off];
+  return bf2f(((const bf16*)v.x)[off]);
+}
+
+__global__ __launch_bounds__(256) void entry_norm_partials(InView v, double* partials) {
+  const int b = blockIdx.y, chunk = blockIdx.x;
+  const long long total = (long long)v.rows * v.cols;
+  const long long per = (total + NORM_CHUNKS - 1) / NORM_CHUNKS;
+  const long long lo = chunk * per;
+  const long long hi = lo + per < total ? lo + per : total;
+  double s = 0.0;
+  for (long long e = lo + threadIdx.x; e < hi; e += blockDim.x) {
+    const int r = (int)(e / v.cols), c = (int)(e - (long long)r * v.cols);
+    const float x = load_in(v, b, r, c);
+    s += (double)x * (double)x;
+  }
+  __shared__ double red[256];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) partials[b * NORM_CHUNKS + chunk] = red[0];
+}
+
+// Pack 64x64 tiles of T-space (i < np rows, j < mp cols).  in_tall: the input is
+// T (rows = n); otherwise it is W (rows = m) and is transposed on the way.
+// scale_mode: 0 none, 1: 1/(||x||+1e-7), 2: 1/(1.01||x||+1e-7).
+__global__ __launch_bounds__(256) void entry_pack(InView v, int in_tall, int scale_mode,
+                                                  const double* partials, int n, int m,
+                                                  int np, int mp, bf16* T, bf16* W) {
+  __shared__ float tile[64][65];
+  const int b = blockIdx.z;
+  const int i0 = blockIdx.y * 64, j0 = blockIdx.x * 64;
+  float scale = 1.f;
+  if (scale_mode) {
+    __shared__ float s_scale;
+    if (threadIdx.x == 0) {
+      double s = 0.0;
+      for (int c = 0; c < NORM_CHUNKS; ++c) s += partials[b * NORM_CHUNKS + c];
+      const float nrm = (float)sqrt(s);
+      const float den = scale_mode == 2 ? nrm * 1.01f + 1e-7f : nrm + 1e-7f;
+      s_scale = den;
+    }
+    __syncthreads();
+    scale = s_scale;
+  }
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  // load in the input's natural orientation (coalesced along its columns)
+  for (int rr = ty; rr < 64; rr += 4) {
+    float x = 0.f;
+    if (in_tall) {
+      const int i = i0 + rr, j = j0 + tx;
+      if (i < n && j < m) x = load_in(v, b, i, j);
+      tile[rr][tx] = x;
+    } else {
+      const int j = j0 + rr, i = i0 + tx;   // W[j][i]
+      if (i < n && j < m) x = load_in(v, b, j, i);
+      tile[tx][rr] = x;
+    }
+  }
+  __syncthreads();
+  bf16* Tb = T + (long long)b * np * mp;
+  bf16* Wb = W + (long long)b * mp * np;
+  for (int rr = ty; rr < 64; rr += 4) {
+    const float xt = scale_mode ? tile[rr][tx] / scale : tile[rr][tx];
+    Tb[(long long)(i0 + rr) * mp + j0 + tx] = f2bf(xt);
+    const float xw = scale_mode ? tile[tx][rr] / scale : tile[tx][rr];
+    Wb[(long long)(j0 + rr) * np + i0 + tx] = f2bf(xw);
+  }
+}
+
+// steps == 0: copy the packed entry out in the input's orientation
+__global__ __launch_bounds__(256) void copy_out(const bf16* T, int np, int mp, int n, int m,
+                                                int out_tall, bf16* out) {
+  const int b = blockIdx.y;
+  const long long total = (long long)n * m;
+  for (long long e = blockIdx.x * 256LL + threadIdx.x; e < total; e += 256LL * gridDim.x) {
+    int i, j;
+    if (out_tall) { i = (int)(e / m); j = (int)(e - (long long)i * m); }
+    else { j = (int)(e / n); i = (int)(e - (long long)j * n); }
+    out[(long long)b * total + e] = T[(long long)b * np * mp + (long long)i * mp + j];
+  }
+}
+
+struct ChainDims {
+  int n, m, np, mp;
+};
+
+static ChainDims chain_dims(int rows, int cols, int orient_tall) {
+  ChainDims d;
+  d.n = orient_tall ? rows : cols;
+  d.m = orient_tall ? cols : rows;
+  d.np = ceil_div(d.n, TILE) * TILE;
+  d.mp = ceil_div(d.m, TILE) * TILE;
+  return d;
+}
+
+static size_t chain_ws_bytes(int batch, const ChainDims& d) {
+  const size_t tw = (size_t)batch * d.np * d.mp * sizeof(bf16);
+  const size_t sq = (size_t)batch * d.mp * d.mp * sizeof(bf16);
+  const size_t part = (size_t)batch * NORM_CHUNKS * sizeof(double);
+  return 4 * tw + 2 * sq + ((part + 255) / 256) * 256;
+}
+
+template <int EPI>
+static int launch_gemm(const GemmArgs& g, int batch, hipStream_t stream, const char* what) {
+  const int per = g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
+  const long long blocks = (long long)per * batch;
+  if (blocks <= 0 || blocks > 0x7fffffffLL) {
+    set_error("%s: bad grid (%lld blocks)", what, blocks);
+    return DMH_EINVAL;
+  }
+  hipLaunchKernelGGL(gemm_nt_bf16<EPI>, dim3((unsigned)blocks), dim3(GEMM_THREADS), 0, stream, g);
+  DMH_CHECK_LAUNCH(what);
+  return DMH_OK;
+}
+
+}  // namespace dmh
+
+using namespace dmh;
+
+extern "C" {
+
+const char* dmh_last_error(void) { return g_err; }
+
+int dmh_ns_workspace_size(int batch, int rows, int cols, int orient_tall, size_t* bytes) {
+  if (batch < 0 || rows <= 0 || cols <= 0 || !bytes) {
+    set_error("dmh_ns_workspace_size: bad arguments");
+    return DMH_EINVAL;
+  }
+  *bytes = chain_ws_bytes(batch, chain_dims(rows, cols, orient_tall));
+  return DMH_OK;
+}
+
+int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int rows, int cols,
+                 long long x_bstride, long long x_rstride, long long x_cstride, void* out,
+                 int orient_tall, int entry_mode, const double* coeffs, int steps, void* ws,
+                 size_t ws_bytes) {
+  if (batch == 0) return DMH_OK;
+  if (!x || !out || batch < 0 || rows <= 0 || cols <= 0 || steps < 0 ||
+      (steps > 0 && !coeffs) || (x_dtype != 0 && x_dtype != 1) || entry_mode < 0 ||
+      entry_mode > 2) {
+    set_error("dmh_ns_chain: bad arguments (batch=%d rows=%d cols=%d steps=%d dtype=%d mode=%d)",
+              batch, rows, cols, steps, x_dtype, entry_mode);
+    return DMH_EINVAL;
+  }
+  const ChainDims d = chain_dims(rows, cols, orient_tall);
+  const size_t need = chain_ws_bytes(batch, d);
+  if (!ws || ws_bytes < need) {
+    set_error("dmh_ns_chain: workspace %zu < %zu bytes", ws_bytes, need);
+    return DMH_EWORKSPACE;
+  }
+  const size_t tw = (size_t)batch * d.np * d.mp;
+  const size_t sq = (size_t)batch * d.mp * d.mp;
+  bf16* T0 = (bf16*)ws;
+  bf16* W0 = T0 + tw;
+  bf16* T1 = W0 + tw;
+  bf16* W1 = T1 + tw;
+  bf16* Am = W1 + tw;
+  bf16* Bm = Am + sq;
+  double* partials = (double*)(Bm + sq);
+
+  InView v{x, x_dtype, x_bstride, x_rstride, x_cstride, rows, cols};
+  if (entry_mode) {
+    hipLaunchKernelGGL(entry_norm_partials, dim3(NORM_CHUNKS, batch), dim3(256), 0, stream, v,
+                       partials);
+    DMH_CHECK_LAUNCH("entry_norm_partials");
+  }
+  hipLaunchKernelGGL(entry_pack, dim3(d.mp / 64, d.np / 64, batch), dim3(256), 0, stream, v,
+                     orient_tall, entry_mode, partials, d.n, d.m, d.np, d.mp, T0, W0);
+  DMH_CHECK_LAUNCH("entry_pack");
+
+  bf16* outp = (bf16*)out;
+  if (steps == 0) {
+    const long long total = (long long)d.n * d.m;
+    const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(copy_out, dim3(blocks, batch), dim3(256), 0, stream, T0, d.np, d.mp, d.n,
+                       d.m, orient_tall, outp);
+    DMH_CHECK_LAUNCH("copy_out");
+    return DMH_OK;
+  }
+
+  const int tm = d.mp / TILE, tn = d.np / TILE;
+  bf16 *Tc = T0, *Wc = W0, *Tn = T1, *Wn = W1;
+  for (int it = 0; it < steps; ++it) {
+    const float a = (float)coeffs[3 * it + 0];
+    const float bcoef = (float)coeffs[3 * it + 1];
+    const float c = (float)coeffs[3 * it + 2];
+    const bool last = it + 1 == steps;
+    int rc;
+    // K1: A = W W^T
+    GemmArgs g1{};
+    g1.P = Wc; g1.p_bs = (long long)d.mp * d.np; g1.p_ld = d.np;
+    g1.Q = Wc; g1.q_bs = g1.p_bs; g1.q_ld = d.np;
+    g1.K = d.np; g1.tiles_m = tm; g1.tiles_n = tm; g1.sym = 1;
+    g1.out = Am; g1.out_bs = (long long)d.mp * d.mp; g1.out_ld = d.mp;
+    g1.outT = Am; g1.outT_bs = g1.out_bs; g1.outT_ld = d.mp;
+    g1.valid_i = d.mp; g1.valid_j = d.mp;
+    if ((rc = launch_gemm<EPI_STORE>(g1, batch, stream, "ns K1 (W W^T)"))) return rc;
+    // K2: B = b A + c A A
+    GemmArgs g2 = g1;
+    g2.P = Am; g2.p_bs = (long long)d.mp * d.mp; g2.p_ld = d.mp;
+    g2.Q = Am; g2.q_bs = g2.p_bs; g2.q_ld = d.mp;
+    g2.K = d.mp;
+    g2.alpha = bcoef; g2.beta = c;
+    g2.aux = Am; g2.aux_bs = g2.p_bs; g2.aux_ld = d.mp;
+    g2.out = Bm; g2.outT = Bm;
+    if ((rc = launch_gemm<EPI_POLY>(g2, batch, stream, "ns K2 (bA + cA^2)"))) return rc;
+    // K3: T' = a T + T B  (and W' = T'^T)
+    GemmArgs g3{};
+    g3.P = Tc; g3.p_bs = (long long)d.np * d.mp; g3.p_ld = d.mp;
+    g3.Q = Bm; g3.q_bs = (long long)d.mp * d.mp; g3.q_ld = d.mp;
+    g3.K = d.mp; g3.tiles_m = tn; g3.tiles_n = tm; g3.sym = 0;
+    g3.alpha = a;
+    g3.aux = Tc; g3.aux_bs = g3.p_bs; g3.aux_ld = d.mp;
+    if (!last) {
+      g3.out = Tn; g3.out_bs = g3.p_bs; g3.out_ld = d.mp;
+      g3.outT = Wn; g3.outT_bs = (long long)d.mp * d.np; g3.outT_ld = d.np;
+      g3.valid_i = d.np; g3.valid_j = d.mp;
+    } else if (orient_tall) {
+      g3.out = outp; g3.out_bs = (long long)d.n * d.m; g3.out_ld = d.m;
+      g3.valid_i = d.n; g3.valid_j = d.m;
+    } else {
+      g3.outT = outp; g3.outT_bs = (long long)d.n * d.m; g3.outT_ld = d.n;
+      g3.valid_i = d.n; g3.valid_j = d.m;
+    }
+    if ((rc = launch_gemm<EPI_AXPY>(g3, batch, stream, "ns K3 (aT + TB)"))) return rc;
+    bf16* t = Tc; Tc = Tn; Tn = t;
+    t = Wc; Wc = Wn; Wn = t;
+  }
+  return DMH_OK;
+}
+
+}  // extern "C"

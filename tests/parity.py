@@ -1,0 +1,46 @@
+"""Parity measures and tolerances shared by the GPU tests.
+
+The bf16 chains amplify rounding differences along directions with small
+singular values, so two correct bf16 implementations with different rounding
+points differ elementwise by a few 1e-2 (the reference's own eager and compiled
+runs differ by 1.7e-2..5e-2 on the same input; tests/test_oracle_golden.py).
+The north-star tolerances are therefore stated on the accuracy measures the
+reference itself reports (spectra/polar_convergence.py:173-174):
+
+  POLAR_TOL   |relerr(gpu, P) - relerr(oracle, P)| with P the exact polar factor
+  ORTH_TOL    relative agreement of ||O^T O - I||_F
+  DIRECT_TOL  ||gpu - oracle||_F / ||oracle||_F, bounded by the reference's own
+              eager-vs-compiled spread
+  SUBSPACE_TOL  fp32 rSVD head subspace / singular values / Frobenius divisor
+"""
+
+import torch
+
+from oracle import polar_oracle as O
+
+POLAR_TOL = 2e-2
+ORTH_TOL = 5e-2
+DIRECT_TOL = 6e-2
+SUBSPACE_TOL = 1e-4
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def assert_polar_parity(got, want, source, tag=""):
+    """got: GPU bf16 output; want: oracle output; source: the fp32 input whose
+    polar factor both approximate (same orientation as got/want)."""
+    got, want, source = got.cpu(), want.cpu(), source.cpu()
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert torch.isfinite(got.float()).all(), f"{tag}: non-finite output"
+    P = O.exact_polar(source)
+    e_got, e_want = O.rel_err(got, P), O.rel_err(want, P)
+    assert abs(e_got - e_want) <= POLAR_TOL, f"{tag}: relerr {e_got:.4f} vs oracle {e_want:.4f}"
+    o_got, o_want = O.orth_residual(got), O.orth_residual(want)
+    assert abs(o_got - o_want) <= ORTH_TOL * o_want + 1e-3, \
+        f"{tag}: orth residual {o_got:.4f} vs oracle {o_want:.4f}"
+    d = rel(got, want)
+    assert d <= DIRECT_TOL, f"{tag}: direct difference {d:.4f}"
+    return dict(relerr=e_got, relerr_oracle=e_want, orth=o_got, orth_oracle=o_want, direct=d)
