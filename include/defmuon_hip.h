@@ -1,0 +1,102 @@
+/*
+ * defmuon_hip.h -- C ABI of the MI355X (gfx950) polar-factor library
+ *                  (libdefmuon_hip.so, built from spectral-deflation_amd/csrc).
+ *
+ * Drop-in boundary for the polar-factor path of deflated Muon in
+ * ComputationalRobotics/Spectral-Deflation.  Each entry point names the reference
+ * function it replaces (paths relative to that tree).
+ *
+ * Conventions
+ *   - All pointers are device pointers; nothing here allocates.  Outputs and the
+ *     workspace are caller-owned; size the workspace with the *_workspace_size
+ *     call for the same shape.
+ *   - Work is enqueued on `stream` (a hipStream_t); no entry point synchronises.
+ *   - Matrices are row-major.  "Tall" batches are (batch, n, m) with n >= m.
+ *   - Return value: 0 on success; 1 bad argument/shape; 2 workspace too small;
+ *     3 HIP launch failure.  dmh_last_error() describes the last failure of the
+ *     calling thread.
+ *   - The sketch width r of the front-end entries is at most 64.
+ */
+#ifndef DEFMUON_HIP_H
+#define DEFMUON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* dmh_stream_t; /* hipStream_t */
+
+/* Text of the calling thread's last error. */
+const char* dmh_last_error(void);
+
+/* ---- bf16 Newton-Schulz / Polar Express chain --------------------------------
+ * Replaces the bf16 GEMM chains of
+ *   zeropower_via_newtonschulz5   defmuon/optim/muon.py:16-44
+ *   PolarExpress                  defmuon/optim/polar_express.py:21-34
+ *   _horner_iterate               defmuon/optim/deflation_batched.py:196-204
+ * for `batch` same-shape matrices in one grouped launch per GEMM phase.
+ *
+ *   x            (batch, rows, cols), element strides (x_bstride, x_rstride,
+ *                x_cstride); x_dtype 0 = fp32, 1 = bf16
+ *   out          (batch, rows, cols) bf16, contiguous
+ *   orient_tall  1: x is the tall operand T (step G = T^T T, T <- aT + T(bG + cG^2),
+ *                the deflated arms' convention); 0: x is the wide operand W
+ *                (A = W W^T, W <- aW + (bA + cA^2) W, muon.py / polar_express.py)
+ *   entry_mode   0: x used as is; 1: x / (||x||_F + 1e-7); 2: x / (1.01 ||x||_F + 1e-7)
+ *                (norm per matrix over the un-rounded input)
+ *   coeffs       steps x 3 doubles (a, b, c) per step
+ */
+int dmh_ns_workspace_size(int batch, int rows, int cols, int orient_tall, size_t* bytes);
+int dmh_ns_chain(dmh_stream_t stream, const void* x, int x_dtype, int batch, int rows, int cols,
+                 long long x_bstride, long long x_rstride, long long x_cstride, void* out,
+                 int orient_tall, int entry_mode, const double* coeffs, int steps, void* ws,
+                 size_t ws_bytes);
+
+/* ---- randomized-SVD deflation front-end (fp32, fp64 Gram) --------------------
+ * One workspace size serves dmh_orth (call it with n = rows, m = r), dmh_project,
+ * dmh_rsvd and dmh_rmfro_clip.
+ */
+int dmh_rsvd_workspace_size(int batch, int n, int m, int r, size_t* bytes);
+int dmh_rmfro_workspace_size(int batch, int n, int m, int r, size_t* bytes);
+
+/* Batched CholeskyQR, `passes` passes: Q = X L^-T with L = chol(X^T X) (fp64).
+ * Replaces _orth_b, defmuon/optim/deflation_batched.py:117-128.
+ * X, Q: (batch, rows, r) fp32.  A non-positive pivot gives Q = 0 for that matrix
+ * (the reference leaves it undefined: cholesky_ex info is ignored). */
+int dmh_orth(dmh_stream_t stream, const float* X, int batch, int rows, int r, int passes,
+             float* Q, void* ws, size_t ws_bytes);
+
+/* Rayleigh-Ritz: thin SVD of Q^T A.  Replaces _project_b,
+ * defmuon/optim/deflation_batched.py:131-139.
+ * Q (batch, n, r), A (batch, n, m) fp32 -> U (batch, n, r), s (batch, r)
+ * descending, V (batch, m, r). */
+int dmh_project(dmh_stream_t stream, const float* Q, const float* A, int batch, int n, int m,
+                int r, float* U, float* s, float* V, void* ws, size_t ws_bytes);
+
+/* Subspace iteration (niter power steps, qr_passes CholeskyQR passes) and
+ * Rayleigh-Ritz on A (batch, n, m) with the caller's sketch Omega (batch, m, r).
+ * Replaces _rsvd_b, defmuon/optim/deflation_batched.py:142-148. */
+int dmh_rsvd(dmh_stream_t stream, const float* A, const float* Omega, int batch, int n, int m,
+             int r, int niter, int qr_passes, float* U, float* s, float* V, void* ws,
+             size_t ws_bytes);
+
+/* The deflation front-end.  Replaces batched_rmfro_clip,
+ * defmuon/optim/deflation_batched.py:155-189 (with Omega injected; the caller
+ * draws it with torch.randn exactly as :172-174 does).
+ *   gate:  kr = #(s > thresh s0); fired = s[kw-1] < ratio s0 && 1 <= kr < r;
+ *          k = fired ? clamp(kr, 1, r-1) : 0                       (k: int64)
+ *   X0 = (A - U_k S_k V_k^T) / d + U_k (1/pad) V_k^T,  d = ||A - U_k S_k V_k^T||_F + 1e-7
+ *   X0: (batch, n, m), bf16 if out_bf16 else fp32; d: (batch,) fp32. */
+int dmh_rmfro_clip(dmh_stream_t stream, const float* A, const float* Omega, int batch, int n,
+                   int m, int r, int kw, float ratio, float thresh, float pad, int niter,
+                   int qr_passes, void* X0, int out_bf16, long long* k, float* d, void* ws,
+                   size_t ws_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DEFMUON_HIP_H */

@@ -27,7 +27,20 @@ _SIGS = {
     "dmh_ns_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
     "dmh_ns_chain": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_ll, c_vp,
                              c_int, c_int, ctypes.POINTER(ctypes.c_double), c_int, c_vp, c_sz]),
+    "dmh_rsvd_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
+    "dmh_rmfro_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
+    "dmh_orth": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_sz]),
+    "dmh_project": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp,
+                            c_vp, c_sz]),
+    "dmh_rsvd": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp, c_vp,
+                         c_vp, c_vp, c_sz]),
+    "dmh_rmfro_clip": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_float,
+                               c_float, c_float, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp,
+                               c_sz]),
 }
+
+# largest sketch width the front-end kernels carry (include/defmuon_hip.h)
+MAX_SKETCH = 64
 
 EXPORTS = tuple(_SIGS)
 
@@ -107,3 +120,87 @@ def ns_chain(X, orient_tall, entry_mode, coeffs, out=None):
                           int(entry_mode), flat, steps, c_vp(ws.data_ptr()), nbytes.value)
     _check(rc, "dmh_ns_chain")
     return out
+
+
+def _ptr(t):
+    return c_vp(t.data_ptr())
+
+
+def _f32c(t, what):
+    _require_gpu(t, what)
+    return t.contiguous() if t.dtype == torch.float32 else t.float().contiguous()
+
+
+def _rsvd_ws(B, n, m, r, device):
+    nbytes = c_sz()
+    _check(load().dmh_rsvd_workspace_size(B, n, m, r, ctypes.byref(nbytes)),
+           "dmh_rsvd_workspace_size")
+    return _workspace(nbytes.value, device), nbytes.value
+
+
+def orth(X, passes=1):
+    """Batched CholeskyQR of X (B, rows, r) fp32 -> Q (B, rows, r)."""
+    X = _f32c(X, "orth")
+    B, rows, r = X.shape
+    Q = torch.empty_like(X)
+    if B == 0:
+        return Q
+    ws, nb = _rsvd_ws(B, rows, r, r, X.device)
+    _check(load().dmh_orth(_stream(X.device), _ptr(X), B, rows, r, int(passes), _ptr(Q),
+                           _ptr(ws), nb), "dmh_orth")
+    return Q
+
+
+def project(Q, A):
+    """Rayleigh-Ritz: thin SVD of Q^T A.  Q (B, n, r), A (B, n, m) fp32 ->
+    U (B, n, r), s (B, r) descending, V (B, m, r)."""
+    Q, A = _f32c(Q, "project"), _f32c(A, "project")
+    B, n, m = A.shape
+    r = Q.shape[-1]
+    U = torch.empty((B, n, r), dtype=torch.float32, device=A.device)
+    s = torch.empty((B, r), dtype=torch.float32, device=A.device)
+    V = torch.empty((B, m, r), dtype=torch.float32, device=A.device)
+    if B == 0:
+        return U, s, V
+    ws, nb = _rsvd_ws(B, n, m, r, A.device)
+    _check(load().dmh_project(_stream(A.device), _ptr(Q), _ptr(A), B, n, m, r, _ptr(U), _ptr(s),
+                              _ptr(V), _ptr(ws), nb), "dmh_project")
+    return U, s, V
+
+
+def rsvd(A, Omega, niter=1, passes=1):
+    """Subspace iteration + Rayleigh-Ritz on A (B, n, m) with sketch Omega (B, m, r)."""
+    A, Omega = _f32c(A, "rsvd"), _f32c(Omega, "rsvd")
+    B, n, m = A.shape
+    r = Omega.shape[-1]
+    U = torch.empty((B, n, r), dtype=torch.float32, device=A.device)
+    s = torch.empty((B, r), dtype=torch.float32, device=A.device)
+    V = torch.empty((B, m, r), dtype=torch.float32, device=A.device)
+    if B == 0:
+        return U, s, V
+    ws, nb = _rsvd_ws(B, n, m, r, A.device)
+    _check(load().dmh_rsvd(_stream(A.device), _ptr(A), _ptr(Omega), B, n, m, r, int(niter),
+                           int(passes), _ptr(U), _ptr(s), _ptr(V), _ptr(ws), nb), "dmh_rsvd")
+    return U, s, V
+
+
+def rmfro_clip(A, Omega, kw, ratio, thresh, pad, niter=1, passes=1, out_dtype=None):
+    """Deflation front-end on A (B, n, m), n >= m: returns (X0, k int64, d fp32).
+    X0 is bf16 when out_dtype is torch.bfloat16, else fp32."""
+    A, Omega = _f32c(A, "rmfro_clip"), _f32c(Omega, "rmfro_clip")
+    B, n, m = A.shape
+    r = Omega.shape[-1]
+    bf = out_dtype == torch.bfloat16
+    X0 = torch.empty((B, n, m), dtype=torch.bfloat16 if bf else torch.float32, device=A.device)
+    k = torch.empty((B,), dtype=torch.int64, device=A.device)
+    d = torch.empty((B,), dtype=torch.float32, device=A.device)
+    if B == 0:
+        return X0, k, d
+    ws, nb = _rsvd_ws(B, n, m, r, A.device)
+    _check(load().dmh_rmfro_clip(_stream(A.device), _ptr(A), _ptr(Omega), B, n, m, r, int(kw),
+                                 float(ratio), float(thresh), float(pad), int(niter),
+                                 int(passes), _ptr(X0), int(bf), _ptr(k), _ptr(d), _ptr(ws), nb),
+           "dmh_rmfro_clip")
+    if out_dtype is not None and not bf and out_dtype != torch.float32:
+        X0 = X0.to(out_dtype)
+    return X0, k, d

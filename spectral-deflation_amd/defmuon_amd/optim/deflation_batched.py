@@ -1,0 +1,177 @@
+"""Batched, gated randomized-SVD deflation front-end and the deflated arms, on the
+HIP C-ABI library.
+
+Drop-in for defmuon/optim/deflation_batched.py.  For a tall momentum batch
+A (B, n, m), n >= m (deflation_batched.py:1-27):
+
+    W   = A - U_k S_k V_k^T          remove the leading outlier directions
+    X0  = W / (||W||_F + 1e-7)       Frobenius entry on the remainder
+    X0 += U_k (1/pad) V_k^T          restore the head at height 1/pad
+
+with (U, s, V) from a Gaussian-sketch subspace iteration (CholeskyQR with an fp64
+Gram, Rayleigh-Ritz) and a gate that declines matrices without outlier
+structure (X0 = A / (||A||_F + 1e-7) there).  The sketch is drawn here with
+torch.randn from the caller's generator, exactly as the reference draws it
+(deflation_batched.py:172-174), so the random stream is torch's; everything
+after the sketch runs in the library on the current stream with no host sync.
+
+Module-level names, environment variables and defaults match the reference
+(deflation_batched.py:42-110) so logs and ablation scripts keep working.
+
+Behaviour the reference leaves undefined: a rank-deficient sketch Gram (e.g. an
+all-zero momentum) makes the reference's cholesky_ex fail silently and its
+output non-finite.  Here such a matrix is declined by the gate (k = 0) and gets
+the plain entry A / (||A||_F + 1e-7), which is finite.
+"""
+
+import math
+import os
+
+import torch
+
+from defmuon_amd import _native
+
+# ---------------------------------------------------------------------------
+# deflation constants (deflation_batched.py:42-59; same env names and defaults)
+# ---------------------------------------------------------------------------
+DIVISOR_PAD = float(os.environ.get("DEFMUON_DEFL_PAD", "1.01"))
+RSVD_NITER = int(os.environ.get("DEFMUON_DEFL_NITER", "1"))
+CHOLQR_PASSES = int(os.environ.get("DEFMUON_DEFL_QR_PASSES", "1"))
+GRAM_DTYPE = torch.float64
+GATE_WINDOW = float(os.environ.get("DEFMUON_DEFL_WINDOW", "0.025"))
+SKETCH_FRAC = float(os.environ.get("DEFMUON_DEFL_SKETCH", str(GATE_WINDOW)))
+OVERSAMPLE_FRAC = float(os.environ.get("DEFMUON_DEFL_OS", "0.025"))
+GATE_RATIO = float(os.environ.get("DEFMUON_DEFL_RATIO", "0.10"))
+DEFLATE_THRESH = float(os.environ.get("DEFMUON_DEFL_THRESH", str(GATE_RATIO)))
+
+# gate statistics: device int64[3] (total, fired, k_sum) ticked by the optimizer
+_GATE_ACC = [None]
+_DEGENERATE = [0]
+_PARACHUTE = [0]
+
+# optional per-call timing, clip vs iteration (DEFMUON_TIME_POLAR=1)
+_TIMING = {"clip_ms": 0.0, "iter_ms": 0.0, "calls": 0}
+_PENDING = []
+_TIMING_ON = [bool(int(os.environ.get("DEFMUON_TIME_POLAR", "0")))]
+
+
+def enable_polar_timing(on=True):
+    _TIMING_ON[0] = bool(on)
+
+
+def flush_timings():
+    """Drain recorded events into the accumulator.  Call only after a sync."""
+    if not _PENDING:
+        return
+    for e0, e1, e2 in _PENDING:
+        _TIMING["clip_ms"] += e0.elapsed_time(e1)
+        _TIMING["iter_ms"] += e1.elapsed_time(e2)
+        _TIMING["calls"] += 1
+    _PENDING.clear()
+
+
+def timing_stats(reset=True):
+    """(clip_ms, iter_ms, calls) accumulated since the last reset."""
+    flush_timings()
+    out = dict(_TIMING)
+    if reset:
+        _TIMING.update(clip_ms=0.0, iter_ms=0.0, calls=0)
+    return out
+
+
+def polar_stats():
+    """Gate firing rate and mean deflation width; the one host read of the
+    device-side accumulator."""
+    if _GATE_ACC[0] is not None:
+        total, fired, k_sum = _GATE_ACC[0].tolist()
+    else:
+        total = fired = k_sum = 0
+    return dict(fired=fired, total=total, k_mean=(k_sum / max(fired, 1)),
+                degenerate=_DEGENERATE[0], parachute=_PARACHUTE[0])
+
+
+# ---------------------------------------------------------------------------
+# batched randomized SVD (library kernels)
+# ---------------------------------------------------------------------------
+
+def sketch_dims(m):
+    """(r, kw): sketch width and gate window (deflation_batched.py:170-171)."""
+    r = min(int(math.ceil(SKETCH_FRAC * m)) + int(math.ceil(OVERSAMPLE_FRAC * m)), m)
+    kw = min(max(1, int(math.ceil(GATE_WINDOW * m))), r)
+    return r, kw
+
+
+def _orth_b(X):
+    """Batched CholeskyQR (CHOLQR_PASSES passes): X (B, n, r) -> Q."""
+    return _native.orth(X, CHOLQR_PASSES)
+
+
+def _project_b(Q, A):
+    """Batched Rayleigh-Ritz: U = Q Ub, s, V from the thin SVD of Q^T A."""
+    return _native.project(Q, A)
+
+
+def _rsvd_b(A, Omega, n_iter):
+    """Batched subspace iteration with `n_iter` power steps, then Rayleigh-Ritz."""
+    return _native.rsvd(A, Omega, n_iter, CHOLQR_PASSES)
+
+
+# ---------------------------------------------------------------------------
+# the deflation front-end (batched remove-then-restore), fp32
+# ---------------------------------------------------------------------------
+
+def batched_rmfro_clip(A, generator=None, Omega=None, out_dtype=None, pad=DIVISOR_PAD):
+    """Remove-then-restore deflation for a batch A (B, n, m), n >= m.
+
+    Returns (X0, k (B,) int64, d (B,) fp32): the deflation entry, the deflation
+    width (0 where the gate declined) and the Frobenius divisor used."""
+    Bn, n, m = A.shape
+    r, kw = sketch_dims(m)
+    if Omega is None:
+        Omega = torch.randn(Bn, m, r, device=A.device, dtype=A.dtype, generator=generator)
+    if r > _native.MAX_SKETCH:
+        raise _native.NativeError(f"sketch width r={r} exceeds the library's {_native.MAX_SKETCH}")
+    return _native.rmfro_clip(A, Omega, kw, GATE_RATIO, DEFLATE_THRESH, pad, RSVD_NITER,
+                              CHOLQR_PASSES, out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# the deflated arms: the setup above, plus a per-arm pad and bf16 iteration
+# ---------------------------------------------------------------------------
+
+def _horner_iterate(X, hs):
+    """X <- aX + bX^3 + cX^5 per (a, b, c) in hs, tall convention
+    (G = X^T X, X <- aX + X(bG + cG^2)), on a (B, n, m) bf16 batch in one grouped
+    launch per GEMM phase."""
+    squeeze = X.ndim == 2
+    Xb = X[None] if squeeze else X
+    out = _native.ns_chain(Xb, True, 0, [tuple(h) for h in hs])
+    return out[0] if squeeze else out
+
+
+class _DeflatedPolarBase:
+    """A deflated arm: the batched fp32 setup, then a subclass-chosen bf16
+    iteration.  Subclasses supply `_iterate`."""
+    PAD = DIVISOR_PAD
+    BATCHED_CLIP = staticmethod(batched_rmfro_clip)
+
+    def _iterate(self, X, steps):
+        raise NotImplementedError
+
+
+class DeflatedNSPolar(_DeflatedPolarBase):
+    """The standard Newton-Schulz quintic behind the deflation."""
+    NS_ABC = (3.4445, -4.7750, 2.0315)
+
+    def _iterate(self, X, steps):
+        return _horner_iterate(X, [self.NS_ABC] * steps)
+
+
+class DeflatedPEPolar(_DeflatedPolarBase):
+    """The Polar Express schedule behind the deflation; PAD defaults to 1.1
+    (DEFMUON_DEFL_PE_PAD)."""
+    PAD = float(os.environ.get("DEFMUON_DEFL_PE_PAD", "1.1"))
+
+    def _iterate(self, X, steps):
+        from defmuon_amd.optim.polar_express import pe_schedule
+        return _horner_iterate(X, pe_schedule(steps))

@@ -1,0 +1,271 @@
+"""Muon with the polar factor on the HIP library.
+
+Drop-in for defmuon/optim/muon.py: the same `zeropower_via_newtonschulz5(G, steps)`
+contract (muon.py:16-44) and the same `Muon` optimizer API, parameter routing,
+W_QKV split, batched deflated step, sketch seeding, gate statistics, learning
+rate scaling and AdamW backup (muon.py:47-438).
+
+One execution difference, with identical per-matrix results: the deflated step
+runs the bf16 iteration once per tall-shape group (one grouped launch per GEMM
+phase over every matrix of the group) instead of once per parameter
+(muon.py:309-312).  Each matrix's iteration is independent of the others in the
+batch, so the outputs are the same matrices the per-parameter calls produce.
+"""
+
+import math
+import os
+
+import torch
+
+from defmuon_amd import _native
+from defmuon_amd.optim.deflation_batched import (_DeflatedPolarBase, _GATE_ACC, _PENDING,
+                                                 _TIMING_ON)
+from defmuon_amd.optim.polar_express import PolarExpress, as_batch
+
+NS_ABC = (3.4445, -4.7750, 2.0315)
+
+
+def zeropower_via_newtonschulz5(G, steps):
+    """Quintic Newton-Schulz polar factor: bf16 output of G's shape.  Entry
+    X / (||X||_F + 1e-7); the chain runs on the transposed matrix when
+    G.size(0) > G.size(1), the reference's own test (muon.py:30)."""
+    assert len(G.shape) >= 2
+    tall = G.size(0) > G.size(1)
+    out = _native.ns_chain(as_batch(G), tall, 1, [NS_ABC] * steps)
+    return out.reshape(G.shape)
+
+
+_EXCLUDED = ("embeddings", "embed_tokens", "wte", "lm_head", "wpe")
+
+
+class Muon(torch.optim.Optimizer):
+    """MomentUm Orthogonalized by Newton-Schulz, with the polar factor computed by
+    the HIP library.
+
+    Arguments (muon.py:78-92): named_params, lr, weight_decay, momentum,
+    nesterov, ns_steps, rms_scaling, nuclear_scaling, polar_method ("ns5" or
+    "polarexpress"; the deflated arms are added by deflation_cutoff.install()),
+    adamw_betas, adamw_eps, polar_args, batched_deflation (accepted and ignored:
+    the batched path is chosen from the factorizer, as in the reference).
+    """
+
+    def __init__(self, named_params, lr=1e-3, weight_decay=0, momentum=0.95, nesterov=True,
+                 ns_steps=5, rms_scaling=True, nuclear_scaling=False, polar_method="ns5",
+                 adamw_betas=(0.95, 0.95), adamw_eps=1e-8, polar_args={},
+                 batched_deflation=False):
+        defaults = dict(lr=lr, weight_decay=weight_decay, momentum=momentum,
+                        nesterov=nesterov, ns_steps=ns_steps, rms_scaling=rms_scaling,
+                        nuclear_scaling=nuclear_scaling, adamw_betas=adamw_betas,
+                        adamw_eps=adamw_eps)
+        muon, muon_names, adamw = [], [], []
+        for name, p in named_params:
+            if p.ndim >= 2 and not any(x in name for x in _EXCLUDED):
+                muon.append(p)
+                muon_names.append(name)
+            else:
+                adamw.append(p)
+        super().__init__(muon + adamw, defaults)
+        for p, name in zip(muon, muon_names):
+            assert p.ndim == 2, p.ndim
+            self.state[p]["use_muon"] = True
+            if name.endswith("attn.c_attn.weight"):
+                self.state[p]["is_W_QKV"] = True
+        for p in adamw:
+            self.state[p]["use_muon"] = False
+
+        self.polar_factorizer = self._initialize_polar_factorizer(polar_method, polar_args)
+        self.batched_deflation = isinstance(self.polar_factorizer, _DeflatedPolarBase)
+        if self.batched_deflation:
+            self._bd_step = 0
+        if os.environ.get("DEFMUON_WARM_POLAR", "1") == "1":
+            self._warm_polar_compile()
+
+    # -- helpers --------------------------------------------------------------
+    def _qkv_split(self, p, g):
+        """A W_QKV gradient (3d x d) is processed as its three d x d blocks."""
+        if self.state[p].get("is_W_QKV", False):
+            return g.reshape(3, g.shape[0] // 3, g.shape[1])
+        return g
+
+    def _warm_polar_compile(self):
+        """Construction-time warm-up (muon.py:167-240): load the library and run
+        each kernel family once on every shape the step will feed it, so first-call
+        costs land before the clock starts.  Zeros for the iteration, randn from a
+        dedicated generator for the clip; the global RNG is never touched."""
+        fac = self.polar_factorizer
+        steps = self.defaults["ns_steps"]
+        try:
+            _native.load()
+            if isinstance(fac, _DeflatedPolarBase):
+                groups, dev = {}, None
+                for group in self.param_groups:
+                    for p in group["params"]:
+                        if self.state[p].get("use_muon"):
+                            A = self._qkv_split(p, p)
+                            nb = A.shape[0] if A.ndim == 3 else 1
+                            n, m = max(A.shape[-2:]), min(A.shape[-2:])
+                            groups[(n, m)] = groups.get((n, m), 0) + nb
+                            dev = p.device
+                for (n, m), cnt in sorted(groups.items()):
+                    g_ = torch.Generator(device=dev)
+                    g_.manual_seed(0)
+                    A = torch.randn((cnt, n, m), dtype=torch.float32, device=dev, generator=g_)
+                    X0, _, _ = fac.BATCHED_CLIP(A, generator=g_, pad=fac.PAD,
+                                                out_dtype=torch.bfloat16)
+                    fac._iterate(torch.zeros_like(X0), steps)
+                    del A, X0
+                if groups:
+                    print(f"warm_polar: warmed the deflated clip and iteration for "
+                          f"{len(groups)} tall-shape groups at construction")
+            else:
+                seen = set()
+                for group in self.param_groups:
+                    for p in group["params"]:
+                        if not self.state[p].get("use_muon"):
+                            continue
+                        shape = tuple(self._qkv_split(p, p).shape)
+                        key = (shape, p.dtype, p.device)
+                        if key not in seen:
+                            seen.add(key)
+                            fac(torch.zeros(shape, dtype=p.dtype, device=p.device), steps)
+                if seen:
+                    print(f"warm_polar: warmed the polar factorizer for {len(seen)} shapes")
+        except Exception as e:   # a failed warm-up only moves first-call cost into step 1
+            print(f"warm_polar: warm-up failed ({e}); step 1 pays the first-call cost")
+
+    def _initialize_polar_factorizer(self, polar_method, polar_args):
+        if polar_method == "ns5":
+            return zeropower_via_newtonschulz5
+        elif polar_method == "polarexpress":
+            return PolarExpress
+        else:
+            raise ValueError(f"Unknown polar method: {polar_method}")
+
+    def adjust_lr_for_muon(self, lr, rms_scaling, nuclear_scaling, param_shape, grad,
+                           grad_sign):
+        scale = 1.0
+        if rms_scaling:
+            fan_out, fan_in = param_shape[:2]
+            scale *= math.sqrt(fan_out / fan_in)
+        if nuclear_scaling:
+            scale *= torch.trace(grad.T @ grad_sign)
+        return lr * scale
+
+    # -- the batched deflated step (muon.py:251-323) ---------------------------
+    def _muon_step_batched(self, group, params, lr, weight_decay, momentum):
+        fac = self.polar_factorizer
+        ns_steps = group["ns_steps"]
+        entries = []
+        for p in params:
+            if p.grad is None:
+                continue
+            state = self.state[p]
+            if "momentum_buffer" not in state:
+                state["momentum_buffer"] = torch.zeros_like(p.grad)
+            buf = state["momentum_buffer"]
+            buf.mul_(momentum).add_(p.grad)
+            g = p.grad.add(buf, alpha=momentum) if group["nesterov"] else buf
+            A = self._qkv_split(p, g).float()
+            if A.ndim == 2:
+                A = A[None]
+            tr = A.shape[-2] < A.shape[-1]
+            if tr:
+                A = A.mT
+            entries.append({"p": p, "g": g, "A": A, "tr": tr, "nb": A.shape[0]})
+
+        shapes = {}
+        for e in entries:
+            shapes.setdefault(tuple(e["A"].shape[-2:]), []).append(e)
+
+        self._bd_step += 1
+        for gi, (shape, es) in enumerate(sorted(shapes.items())):
+            A = torch.cat([e["A"] for e in es], dim=0)
+            gen = torch.Generator(device=A.device)
+            gen.manual_seed((self._bd_step * 1009 + gi * 9176867) % (2 ** 62))
+            timed = _TIMING_ON[0] and A.is_cuda
+            if timed:
+                e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+                e0.record()
+            X0, kvec, _ = fac.BATCHED_CLIP(A, generator=gen, pad=fac.PAD,
+                                           out_dtype=torch.bfloat16)
+            if timed:
+                e1.record()
+            if _GATE_ACC[0] is None or _GATE_ACC[0].device != kvec.device:
+                _GATE_ACC[0] = torch.zeros(3, dtype=torch.int64, device=kvec.device)
+            _GATE_ACC[0] += torch.stack([
+                torch.tensor(A.shape[0], dtype=torch.int64, device=kvec.device),
+                (kvec > 0).sum(), kvec.sum().to(torch.int64)])
+            Ug = fac._iterate(X0, ns_steps)          # one grouped launch per GEMM phase
+            off = 0
+            for e in es:
+                e["u"] = Ug[off:off + e["nb"]]
+                off += e["nb"]
+            if timed:
+                e2.record()
+                _PENDING.append((e0, e1, e2))
+            for e in es:
+                p, g = e["p"], e["g"]
+                u = (e["u"].mT if e["tr"] else e["u"]).reshape(p.shape).bfloat16()
+                adjusted_lr = self.adjust_lr_for_muon(lr, group["rms_scaling"],
+                                                      group["nuclear_scaling"], p.shape,
+                                                      g.bfloat16(), u)
+                p.data.mul_(1 - lr * weight_decay)
+                p.data.add_(u, alpha=-adjusted_lr)
+
+    # -- step (muon.py:334-438) ------------------------------------------------
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        for group in self.param_groups:
+            params = [p for p in group["params"] if self.state[p]["use_muon"]]
+            lr = group["lr"]
+            weight_decay = group["weight_decay"]
+            momentum = group["momentum"]
+            if self.batched_deflation and params:
+                self._muon_step_batched(group, params, lr, weight_decay, momentum)
+                params = []
+            for p in params:
+                g = p.grad
+                if g is None:
+                    continue
+                state = self.state[p]
+                if "momentum_buffer" not in state:
+                    state["momentum_buffer"] = torch.zeros_like(g)
+                buf = state["momentum_buffer"]
+                buf.mul_(momentum).add_(g)
+                g = g.add(buf, alpha=momentum) if group["nesterov"] else buf
+                old_shape = g.shape
+                g = self._qkv_split(p, g)
+                u = self.polar_factorizer(g, group["ns_steps"])
+                g = g.reshape(old_shape)
+                u = u.reshape(old_shape)
+                adjusted_lr = self.adjust_lr_for_muon(lr, group["rms_scaling"],
+                                                      group["nuclear_scaling"], p.shape,
+                                                      g.bfloat16(), u)
+                p.data.mul_(1 - lr * weight_decay)
+                p.data.add_(u, alpha=-adjusted_lr)
+
+            params = [p for p in group["params"] if not self.state[p]["use_muon"]]
+            beta1, beta2 = group["adamw_betas"]
+            eps = group["adamw_eps"]
+            for p in params:
+                g = p.grad
+                if g is None:
+                    continue
+                state = self.state[p]
+                if "step" not in state:
+                    state["step"] = 0
+                    state["moment1"] = torch.zeros_like(g)
+                    state["moment2"] = torch.zeros_like(g)
+                state["step"] += 1
+                step = state["step"]
+                buf1, buf2 = state["moment1"], state["moment2"]
+                buf1.lerp_(g, 1 - beta1)
+                buf2.lerp_(g.square(), 1 - beta2)
+                g = buf1 / (eps + buf2.sqrt())
+                scale = (1 - beta1 ** step) / (1 - beta2 ** step) ** 0.5
+                p.data.mul_(1 - lr * weight_decay)
+                p.data.add_(g, alpha=-lr / scale)
+        return loss

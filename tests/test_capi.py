@@ -1,0 +1,66 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point that
+include/defmuon_hip.h declares, and its host-side argument checks work (no
+kernel is launched here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "defmuon_hip.h")).read()
+    return sorted(set(re.findall(r"\b(dmh_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from defmuon_amd import _native
+    return _native.load()
+
+
+def test_exports_match_header(lib):
+    from defmuon_amd import _native
+    declared = _declared()
+    assert declared, "no declarations found"
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(_native.EXPORTS) == declared
+
+
+def test_ns_workspace_size(lib):
+    n = ctypes.c_size_t()
+    assert lib.dmh_ns_workspace_size(2, 300, 700, 0, ctypes.byref(n)) == 0
+    mp, np_ = 512, 768          # 300 -> 512, 700 -> 768 (256 tiles)
+    want = 4 * 2 * np_ * mp * 2 + 2 * 2 * mp * mp * 2 + 256 * ((2 * 64 * 8 + 255) // 256)
+    assert n.value == want
+    assert lib.dmh_ns_workspace_size(1, 0, 5, 0, ctypes.byref(n)) == 1
+    assert b"bad arguments" in lib.dmh_last_error()
+
+
+def test_rsvd_workspace_limits(lib):
+    n = ctypes.c_size_t()
+    assert lib.dmh_rsvd_workspace_size(3, 5120, 1280, 64, ctypes.byref(n)) == 0
+    assert n.value > 3 * 5120 * 64 * 4
+    assert lib.dmh_rsvd_workspace_size(3, 5120, 1280, 65, ctypes.byref(n)) == 1
+    assert b"unsupported shape" in lib.dmh_last_error()
+    assert lib.dmh_rsvd_workspace_size(3, 100, 200, 8, ctypes.byref(n)) == 1   # n < m
+
+
+def test_entry_points_reject_bad_arguments_without_launching(lib):
+    from defmuon_amd import _native
+    v = ctypes.c_void_p(0)
+    # null pointers / bad shapes are refused before any HIP call
+    assert lib.dmh_rmfro_clip(v, None, None, 1, 10, 5, 2, 1, 0.1, 0.1, 1.01, 1, 1, None, 1,
+                              None, None, None, 0) == 1
+    coeffs = (ctypes.c_double * 3)(1, 0, 0)
+    assert lib.dmh_ns_chain(v, None, 0, 1, 8, 8, 64, 8, 1, None, 0, 1, coeffs, 1, None, 0) == 1
+    dummy = ctypes.c_void_p(16)
+    assert lib.dmh_ns_chain(v, dummy, 0, 1, 8, 8, 64, 8, 1, dummy, 0, 1, coeffs, 1, dummy,
+                            16) == 2
+    assert b"workspace" in lib.dmh_last_error()
+    # batch 0 is a no-op
+    assert lib.dmh_orth(v, None, 0, 10, 2, 1, None, None, 0) == 0

@@ -1,0 +1,162 @@
+"""GPU parity of the rSVD deflation front-end (dmh_orth / dmh_project / dmh_rsvd /
+dmh_rmfro_clip) against the CPU oracle and the reference's own vectors."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_from_bits
+from oracle import polar_oracle as O
+from parity import SUBSPACE_TOL, rel
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def N():
+    from defmuon_amd import _native
+    _native.load()
+    assert torch.cuda.is_available()
+    return _native
+
+
+def _spiked_batch(shapes_seeds):
+    from defmuon_amd import synthetic as S
+    return torch.stack([S.spiked_matrix(*a, **kw) for a, kw in shapes_seeds])
+
+
+def _head_proj(U, s, V, k):
+    """Sign-invariant head: U_k diag(s_k) V_k^T (fp64)."""
+    U, s, V = U.double().cpu(), s.double().cpu(), V.double().cpu()
+    return (U[..., :k] * s[..., None, :k]) @ V[..., :k].mT
+
+
+def test_orth_matches_oracle(N):
+    X = torch.randn(3, 500, 40, generator=torch.Generator().manual_seed(1))
+    Q = N.orth(X.to(DEV), 1).cpu()
+    Qo = O.orth_b(X)
+    assert float((Q - Qo).abs().max()) < 1e-4
+    I = torch.eye(40)
+    assert float((Q.mT @ Q - I).abs().max()) < 1e-4
+
+
+def test_orth_two_passes(N):
+    X = torch.randn(2, 300, 24, generator=torch.Generator().manual_seed(2))
+    Q = N.orth(X.to(DEV), 2).cpu()
+    Qo = O.orth_b(X, passes=2)
+    assert float((Q - Qo).abs().max()) < 1e-4
+
+
+def test_project_matches_oracle(N):
+    A = _spiked_batch([((600, 200), dict(seed=3, n_spikes=3, hi=40.0, lo=10.0))])
+    Q = O.orth_b(A @ torch.randn(1, 200, 10, generator=torch.Generator().manual_seed(4)))
+    U, s, V = N.project(Q.to(DEV), A.to(DEV))
+    Uo, so, Vo = O.project_b(Q, A)
+    np.testing.assert_allclose(s.cpu().numpy(), so.numpy(), rtol=SUBSPACE_TOL)
+    assert rel(_head_proj(U, s, V, 10), _head_proj(Uo, so, Vo, 10)) < SUBSPACE_TOL
+
+
+@pytest.mark.parametrize("key", ["clip", "clip2"])
+def test_rsvd_matches_reference_vectors(N, golden, key):
+    A = torch.from_numpy(golden["inputs"][f"{key}_A"])
+    Om = torch.from_numpy(golden["inputs"][f"{key}_Omega"])
+    ref = golden["eager"]
+    U, s, V = N.rsvd(A.to(DEV), Om.to(DEV), 1, 1)
+    np.testing.assert_allclose(s.cpu().numpy(), ref[f"{key}_s"], rtol=SUBSPACE_TOL, atol=1e-6)
+    # head subspace where the gate fires (a declined, pure-bulk matrix has no
+    # separated head, so its leading vectors are not determined to 1e-4)
+    Uo, so, Vo = O.rsvd_b(A, Om)
+    for b, k in enumerate(ref[f"{key}_k"].tolist()):
+        if k == 0:
+            continue
+        got = (U[b, :, :k] @ V[b, :, :k].mT).double().cpu()
+        if k == 2:
+            assert rel(got, torch.from_numpy(ref[f"{key}_head_proj"][b]).double()) < SUBSPACE_TOL
+        assert rel(got, (Uo[b, :, :k] @ Vo[b, :, :k].mT).double()) < SUBSPACE_TOL
+
+
+@pytest.mark.parametrize("key", ["clip", "clip2"])
+def test_clip_matches_reference_vectors(N, golden, key):
+    A = torch.from_numpy(golden["inputs"][f"{key}_A"])
+    Om = torch.from_numpy(golden["inputs"][f"{key}_Omega"])
+    ref = golden["eager"]
+    r, kw = O.sketch_dims(A.shape[-1])
+    X0, k, d = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
+                            O.DIVISOR_PAD, 1, 1, None)
+    assert k.cpu().tolist() == ref[f"{key}_k"].tolist()
+    np.testing.assert_allclose(d.cpu().numpy(), ref[f"{key}_d"], rtol=1e-5)
+    assert rel(X0, torch.from_numpy(ref[f"{key}_X0f32"])) < SUBSPACE_TOL
+    X0b, kb, _ = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
+                              O.PE_PAD, 1, 1, torch.bfloat16)
+    assert kb.cpu().tolist() == ref[f"{key}_kpe"].tolist()
+    want = bf16_from_bits(ref[f"{key}_X0pe"])
+    assert rel(X0b, want) < 4e-3           # bf16 rounding of an fp32 result within 1e-4
+    eq = (X0b.cpu().view(torch.int16) == want.view(torch.int16)).float().mean().item()
+    assert eq > 0.97
+
+
+def test_config2_clip(N):
+    """one spiked 3072x768 tall momentum, r=40, kw=20, k=8."""
+    from defmuon_amd import synthetic as S
+    A = S.spiked_matrix(3072, 768, seed=0)[None]
+    r, kw = O.sketch_dims(768)
+    assert (r, kw) == (40, 20)
+    Om = O.draw_omega(1, 768, r, 123)
+    X0, k, d = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
+                            O.DIVISOR_PAD, 1, 1, torch.bfloat16)
+    Xo, ko, do = O.rmfro_clip(A, Om, out_dtype=torch.bfloat16)
+    assert int(k[0]) == int(ko[0]) == 8
+    assert abs(float(d[0]) - float(do[0])) / float(do[0]) < SUBSPACE_TOL
+    assert rel(X0, Xo) < 4e-3
+    U, s, V = N.rsvd(A.to(DEV), Om.to(DEV), 1, 1)
+    Uo, so, Vo = O.rsvd_b(A, Om)
+    np.testing.assert_allclose(s.cpu().numpy()[0, :8], so.numpy()[0, :8], rtol=SUBSPACE_TOL)
+    assert rel(_head_proj(U, s, V, 8), _head_proj(Uo, so, Vo, 8)) < SUBSPACE_TOL
+    # The same algorithm in fp64 is the yardstick: single-pass CholeskyQR in fp32
+    # loses ~kappa * eps of orthogonality on the power-iterated sketch, in the
+    # reference arithmetic as here.  The library must be no less accurate.
+    U8, s8, V8 = O.rsvd_b(A.double(), Om.double())
+    _, _, d8 = O.rmfro_clip(A.double(), Om.double())
+    e_lib = rel(_head_proj(U, s, V, 8), _head_proj(U8, s8, V8, 8))
+    e_ref = rel(_head_proj(Uo, so, Vo, 8), _head_proj(U8, s8, V8, 8))
+    assert e_lib <= 2 * e_ref + 1e-6, (e_lib, e_ref)
+    dd_lib = abs(float(d[0]) - float(d8[0])) / float(d8[0])
+    dd_ref = abs(float(do[0]) - float(d8[0])) / float(d8[0])
+    assert dd_lib <= 2 * dd_ref + 1e-6, (dd_lib, dd_ref)
+
+
+def test_gate_identity_mixed_batch(N):
+    """Config-4 style design at reduced size: 16 spikes 100x..5x (k = 12) and
+    every 4th matrix with no spike (k = 0); gate decisions identical to the
+    oracle's."""
+    spec = []
+    for i in range(8):
+        ns = 0 if i % 4 == 3 else 16
+        spec.append(((1536, 768), dict(seed=100 + i, n_spikes=ns, hi=100.0, lo=5.0)))
+    A = _spiked_batch(spec)
+    r, kw = O.sketch_dims(768)
+    Om = O.draw_omega(8, 768, r, 77)
+    _, k, d = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
+                           O.PE_PAD, 1, 1, torch.bfloat16)
+    _, ko, do = O.rmfro_clip(A, Om, pad=O.PE_PAD)
+    assert k.cpu().tolist() == ko.tolist() == [12, 12, 12, 0, 12, 12, 12, 0]
+    np.testing.assert_allclose(d.cpu().numpy(), do.numpy(), rtol=SUBSPACE_TOL)
+
+
+def test_zero_matrix_is_declined_and_finite(N):
+    """A rank-deficient sketch Gram: the reference is undefined (NaN); the
+    library declines the matrix and returns the plain entry (zeros here)."""
+    from defmuon_amd import synthetic as S
+    A = torch.stack([torch.zeros(400, 200), S.spiked_matrix(400, 200, seed=5, n_spikes=2,
+                                                            hi=40.0, lo=20.0)])
+    r, kw = O.sketch_dims(200)
+    Om = O.draw_omega(2, 200, r, 9)
+    X0, k, d = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
+                            O.DIVISOR_PAD, 1, 1, torch.bfloat16)
+    assert torch.isfinite(X0.float()).all()
+    assert int(k[0]) == 0 and float(X0[0].float().abs().max()) == 0.0
+    assert int(k[1]) == 2
+    _, ko, _ = O.rmfro_clip(A[1:], Om[1:])
+    assert int(ko[0]) == 2

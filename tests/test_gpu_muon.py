@@ -1,0 +1,179 @@
+"""GPU parity of the drop-in Muon optimizer (all four arms) against a CPU
+restatement of the reference's step built from the oracle (muon.py:251-402)."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import polar_oracle as O
+from parity import DIRECT_TOL, assert_polar_parity, rel
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+D = 128          # model width: m = 128 -> r = 8, kw = 4
+LAYERS = 2
+
+
+def _named_params(seed):
+    """A GPT-2-shaped parameter set (nn.Linear (out, in) layout, gpt_model.py)."""
+    g = torch.Generator().manual_seed(seed)
+    shapes = {"wte.weight": (512, D), "wpe.weight": (64, D)}
+    for i in range(LAYERS):
+        shapes[f"h.{i}.ln_1.weight"] = (D,)
+        shapes[f"h.{i}.attn.c_attn.weight"] = (3 * D, D)
+        shapes[f"h.{i}.attn.c_proj.weight"] = (D, D)
+        shapes[f"h.{i}.mlp.c_fc.weight"] = (4 * D, D)
+        shapes[f"h.{i}.mlp.c_proj.weight"] = (D, 4 * D)
+    return {k: torch.nn.Parameter((torch.randn(*v, generator=g) * 0.02).to(DEV))
+            for k, v in shapes.items()}
+
+
+def _grads(params, seed):
+    """Spiked gradients for the Muon matrices (2 spikes each: k = 2 where the
+    gate sees them), Gaussian for the rest.  QKV blocks are spiked per block."""
+    from defmuon_amd import synthetic as S
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for i, (name, p) in enumerate(params.items()):
+        if p.ndim < 2 or "wte" in name or "wpe" in name:
+            out[name] = torch.randn(*p.shape, generator=g) * 1e-2
+        elif "c_attn" in name:
+            out[name] = torch.cat([S.spiked_matrix(D, D, seed=seed * 100 + 10 * i + j,
+                                                   n_spikes=2, hi=50.0, lo=20.0)
+                                   for j in range(3)])
+        else:
+            rows, cols = p.shape
+            out[name] = S.spiked_matrix(rows, cols, seed=seed * 100 + i, n_spikes=2,
+                                        hi=50.0, lo=20.0)
+    return {k: v.to(DEV) for k, v in out.items()}
+
+
+def _expected_updates(params, grads, arm, bd_step, momentum=0.95, steps=5):
+    """The reference's Muon update directions u per parameter (muon.py:266-318 for
+    the deflated arms, :361-386 for the plain ones), computed with the oracle on
+    the CPU.  Sketches are drawn on the GPU with the reference's seed formula."""
+    entries = []
+    for name, p in params.items():
+        if p.ndim < 2 or any(x in name for x in ("wte", "wpe")):
+            continue
+        gr = grads[name].cpu()
+        buf = gr.clone()                       # first step: buf = 0 * m + g
+        g = gr + momentum * buf                # nesterov
+        entries.append((name, p, g))
+    ups = {}
+    if arm in ("ns5", "polarexpress"):
+        for name, p, g in entries:
+            gq = g.reshape(3, D, D) if name.endswith("attn.c_attn.weight") else g
+            fn = O.ns5 if arm == "ns5" else O.polar_express
+            ups[name] = fn(gq, steps).reshape(p.shape), g
+        return ups, None
+    groups = {}
+    for name, p, g in entries:
+        A = g.reshape(3, D, D) if name.endswith("attn.c_attn.weight") else g[None]
+        tr = A.shape[-2] < A.shape[-1]
+        if tr:
+            A = A.mT
+        groups.setdefault(tuple(A.shape[-2:]), []).append((name, p, g, A, tr))
+    stats = [0, 0, 0]
+    pad = O.DIVISOR_PAD if arm == "deflated_ns_cut" else O.PE_PAD
+    hs = O.ns_schedule(steps) if arm == "deflated_ns_cut" else O.pe_schedule(steps)
+    for gi, (shape, es) in enumerate(sorted(groups.items())):
+        A = torch.cat([e[3] for e in es])
+        r, _ = O.sketch_dims(shape[1])
+        Om = O.draw_omega(A.shape[0], shape[1], r, O.group_seed(bd_step, gi), device=DEV).cpu()
+        X0, k, _ = O.rmfro_clip(A, Om, pad=pad, out_dtype=torch.bfloat16)
+        stats[0] += A.shape[0]
+        stats[1] += int((k > 0).sum())
+        stats[2] += int(k.sum())
+        Ug = O.horner_iterate(X0, hs)
+        off = 0
+        for name, p, g, Ae, tr in es:
+            u = Ug[off:off + Ae.shape[0]]
+            off += Ae.shape[0]
+            ups[name] = ((u.mT if tr else u).reshape(p.shape), g)
+    return ups, stats
+
+
+@pytest.fixture(scope="module")
+def muon_mod():
+    from defmuon_amd.optim import deflation_batched as DB
+    from defmuon_amd.optim import deflation_cutoff
+    from defmuon_amd.optim import muon
+    deflation_cutoff.install()
+    return muon, DB
+
+
+@pytest.mark.parametrize("arm", ["ns5", "polarexpress", "deflated_ns_cut", "deflated_pe_cut"])
+def test_muon_step_matches_reference(muon_mod, arm):
+    muon, DB = muon_mod
+    params = _named_params(1)
+    grads = _grads(params, 2)
+    before = {k: v.detach().clone() for k, v in params.items()}
+    DB._GATE_ACC[0] = None
+    opt = muon.Muon(list(params.items()), lr=0.01, weight_decay=0.0, momentum=0.95,
+                    nesterov=True, ns_steps=5, polar_method=arm)
+    assert opt.batched_deflation == arm.startswith("deflated")
+    for k, p in params.items():
+        p.grad = grads[k]
+    opt.step()
+    torch.cuda.synchronize()
+    ups, stats = _expected_updates(params, grads, arm, bd_step=1)
+    for name, (u_ref, g) in ups.items():
+        p = params[name]
+        fan_out, fan_in = p.shape
+        alr = 0.01 * math.sqrt(fan_out / fan_in)
+        u_got = ((before[name] - p.detach()) / alr).cpu()
+        src = g.reshape(3, D, D) if name.endswith("attn.c_attn.weight") else g
+        got = u_got.reshape(src.shape) if src.ndim == 3 else u_got
+        want = u_ref.reshape(src.shape).float() if src.ndim == 3 else u_ref.float()
+        if src.ndim == 3:
+            for j in range(3):
+                assert_polar_parity(got[j], want[j], src[j], f"{arm} {name}[{j}]")
+        else:
+            assert_polar_parity(got, want, src, f"{arm} {name}")
+    if stats is not None:
+        st = DB.polar_stats()
+        assert [st["total"], st["fired"]] == stats[:2]
+        assert st["k_mean"] == stats[2] / max(stats[1], 1)
+        assert st["degenerate"] == 0 and st["parachute"] == 0
+    # AdamW parameters moved by the AdamW rule
+    assert not torch.equal(before["wte.weight"], params["wte.weight"].detach())
+
+
+def test_timing_and_second_step(muon_mod):
+    """Event timing records clip vs iteration; a second step uses bd_step 2."""
+    muon, DB = muon_mod
+    params = _named_params(3)
+    grads = _grads(params, 4)
+    opt = muon.Muon(list(params.items()), lr=0.01, polar_method="deflated_ns_cut")
+    DB.enable_polar_timing(True)
+    try:
+        for _ in range(2):
+            for k, p in params.items():
+                p.grad = grads[k]
+            opt.step()
+        torch.cuda.synchronize()
+        t = DB.timing_stats()
+    finally:
+        DB.enable_polar_timing(False)
+    assert opt._bd_step == 2
+    assert t["calls"] == 4 and t["clip_ms"] > 0 and t["iter_ms"] > 0
+
+
+def test_cutoff_switches_to_plain_arm(muon_mod, monkeypatch):
+    muon, DB = muon_mod
+    from defmuon_amd.optim import deflation_cutoff as C
+    monkeypatch.setattr(C, "CUTOFF_STEPS", 1)
+    params = _named_params(5)
+    grads = _grads(params, 6)
+    opt = muon.Muon(list(params.items()), lr=0.01, polar_method="deflated_pe_cut")
+    assert opt.batched_deflation
+    for _ in range(2):
+        for k, p in params.items():
+            p.grad = grads[k]
+        opt.step()
+    assert not opt.batched_deflation
+    from defmuon_amd.optim.polar_express import PolarExpress
+    assert opt.polar_factorizer is PolarExpress
