@@ -1,0 +1,233 @@
+#!/usr/bin/env python
+"""Polar steps per second of deflated Muon's polar-factor path on one MI355X.
+
+A polar step is what Muon._muon_step_batched does between stacking the momenta
+and applying the update (muon.py:288-315): for every tall-shape group, seed the
+sketch generator from (step, group), run BATCHED_CLIP (Gaussian sketch, rSVD,
+gate, deflate/restore to bf16), tick the gate counters, and run the arm's 5-step
+bf16 iteration over the whole group.  Inputs are synthetic spiked-spectrum fp32
+momenta already resident in HBM (8 spikes 50x..10x over a Marchenko-Pastur
+bulk, Haar singular vectors).
+
+    python bench.py [--steps K] [--warmup W] [--workload gpt2-large] [--arm deflated_ns_cut]
+
+prints one JSON line.  `roofline` covers the NS chain (the dominant work): its
+canonical dense bf16 FLOPs per polar step over the time of its launches, taken
+with HIP events on the launch stream inside the timed region.  `cpu_baseline`
+times the CPU restatement of the reference arithmetic (oracle/) on a bounded
+sample of the same workload and extrapolates to the full step.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "spectral-deflation_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+# tall-shape groups (batch, n, m) of one polar step, after the W_QKV split and the
+# wide -> tall transpose (muon.py:275-285); GPT-2 Linear weights are (out, in)
+WORKLOADS = {
+    "gpt2-small": [(48, 768, 768), (24, 3072, 768)],
+    "gpt2-medium": [(96, 1024, 1024), (48, 4096, 1024)],
+    "gpt2-large": [(144, 1280, 1280), (72, 5120, 1280)],
+}
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def ns_flops(groups, steps=5):
+    """Canonical dense NS FLOPs: 4 m^2 n + 2 m^3 per matrix and iteration."""
+    return sum(B * steps * (4 * m * m * n + 2 * m ** 3) for B, n, m in groups)
+
+
+def make_inputs(groups, device, seed=1234):
+    from defmuon_amd import synthetic as S
+    out = []
+    for gi, (B, n, m) in enumerate(groups):
+        out.append(S.spiked_batch(B, n, m, seed=seed + gi, n_spikes=8, hi=50.0, lo=10.0,
+                                  device=device))
+    return out
+
+
+def polar_step(fac, stacks, bd_step, ns_steps, events=None):
+    """One polar step over all groups; returns per-group (U, k)."""
+    import torch
+    from defmuon_amd.optim import deflation_batched as DB
+    outs = []
+    for gi, A in enumerate(stacks):
+        gen = torch.Generator(device=A.device)
+        gen.manual_seed((bd_step * 1009 + gi * 9176867) % (2 ** 62))
+        X0, kvec, _ = fac.BATCHED_CLIP(A, generator=gen, pad=fac.PAD, out_dtype=torch.bfloat16)
+        if DB._GATE_ACC[0] is None:
+            DB._GATE_ACC[0] = torch.zeros(3, dtype=torch.int64, device=A.device)
+        DB._GATE_ACC[0] += torch.stack([
+            torch.tensor(A.shape[0], dtype=torch.int64, device=A.device),
+            (kvec > 0).sum(), kvec.sum().to(torch.int64)])
+        if events is not None:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+        U = fac._iterate(X0, ns_steps)
+        if events is not None:
+            e1 = torch.cuda.Event(enable_timing=True)
+            e1.record()
+            events.append((e0, e1))
+        outs.append((U, kvec))
+    return outs
+
+
+def cpu_baseline(groups, arm, min_s=12.0, max_reps=20):
+    """Time the oracle (CPU restatement of the reference arithmetic) on single
+    matrices of each group -- one warm-up, then repeats until about min_s seconds
+    of CPU work -- and extrapolate by batch size to the full step."""
+    import torch
+    from defmuon_amd import synthetic as S
+    from oracle import polar_oracle as O
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    hs = O.ns_schedule(5) if arm == "deflated_ns_cut" else O.pe_schedule(5)
+    pad = O.DIVISOR_PAD if arm == "deflated_ns_cut" else O.PE_PAD
+    per_matrix, reps = [], []
+    for gi, (B, n, m) in enumerate(groups):
+        A = S.spiked_batch(1, n, m, seed=99 + gi)
+        r, _ = O.sketch_dims(m)
+        Om = O.draw_omega(1, m, r, 7)
+        times, spent = [], 0.0
+        for rep in range(max_reps + 1):
+            t0 = time.perf_counter()
+            X0, _, _ = O.rmfro_clip(A, Om, pad=pad, out_dtype=torch.bfloat16)
+            O.horner_iterate(X0, hs)
+            dt = time.perf_counter() - t0
+            if rep > 0:
+                times.append(dt)
+                spent += dt
+            if rep >= 3 and spent > min_s / len(groups):
+                break
+        times.sort()
+        per_matrix.append(times[len(times) // 2])
+        reps.append(len(times))
+        log(f"cpu_baseline: group {gi} ({n}x{m}) median {per_matrix[-1]:.3f} s per matrix "
+            f"over {len(times)} runs")
+    t_step = sum(B * t for (B, _, _), t in zip(groups, per_matrix))
+    return {"value": 1.0 / t_step, "unit": "polar_steps/s", "cores": cores, "kind": "port",
+            "sample": ("oracle/ (torch CPU restatement of the reference arithmetic, "
+                       f"arm {arm}, torch.set_num_threads({cores})): single matrices of "
+                       f"each shape group, median of {reps} runs after a warm-up, "
+                       f"extrapolated by batch size to the full step ({t_step:.2f} s per "
+                       "step)"),
+            "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="gpt2-large", choices=sorted(WORKLOADS))
+    ap.add_argument("--arm", default="deflated_ns_cut",
+                    choices=["deflated_ns_cut", "deflated_pe_cut"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the polar path "
+              "shards by matrix across GPUs, which this build does not run.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from defmuon_amd import _native
+    from defmuon_amd.optim import deflation_batched as DB
+    from defmuon_amd.optim import deflation_cutoff as C
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    _native.load()
+    dev = torch.device("cuda", 0)
+    groups = WORKLOADS[args.workload]
+    fac = C.ARMS[args.arm]()
+    log(f"bench: generating inputs for {args.workload}: {groups}")
+    stacks = make_inputs(groups, dev)
+    torch.cuda.synchronize()
+
+    log(f"bench: warmup {args.warmup}")
+    for w in range(args.warmup):
+        polar_step(fac, stacks, w + 1, 5)
+    torch.cuda.synchronize()
+    DB._GATE_ACC[0] = None
+
+    log(f"bench: timing {args.steps} steps")
+    events = []
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(args.steps):
+        polar_step(fac, stacks, args.warmup + s + 1, 5, events)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(stop)
+    ms_per_step = gpu_ms / args.steps
+    ns_ms = sum(a.elapsed_time(b) for a, b in events) / args.steps
+    st = DB.polar_stats()
+    flops = ns_flops(groups)
+    achieved = flops / (ns_ms * 1e-3) / 1e12
+    log(f"bench: {ms_per_step:.3f} ms/step (wall {1e3 * wall / args.steps:.3f}), NS chain "
+        f"{ns_ms:.3f} ms, gate {st}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline")
+        cpu = cpu_baseline(groups, args.arm)
+
+    nmat = sum(B for B, _, _ in groups)
+    out = {
+        "metric": "polar steps/sec (GPT-2-large all matrices, 1 GPU) + % bf16 MFMA peak",
+        "value": 1e3 / ms_per_step,
+        "unit": "polar_steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 (NS chain) / fp32+fp64 (rSVD front-end)",
+        "data": "synthetic: spiked-spectrum fp32 momenta (8 spikes 50x..10x over a "
+                "Marchenko-Pastur bulk, Haar singular vectors), resident in HBM",
+        "config": {"workload": f"{args.workload} {args.arm} polar step: "
+                               + " + ".join(f"{B}x({n},{m})" for B, n, m in groups),
+                   "matrices": nmat, "ns_steps": 5, "arm": args.arm},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "kernel": "NS chain (gemm_nt_bf16 phases + entry_pack), "
+                               "canonical dense 4m^2n+2m^3 FLOP per matrix-iteration",
+                     "flops_per_step": flops, "ns_ms_per_step": ns_ms},
+        "frontend_ms_per_step": ms_per_step - ns_ms,
+        "gate": st,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -76,3 +76,51 @@ def expected_k(n_spikes, hi, lo, thresh=0.10):
         return 0
     vals = [hi * (lo / hi) ** (i / max(n_spikes - 1, 1)) for i in range(n_spikes)]
     return sum(1 for v in vals if v > thresh * vals[0])
+
+
+def mp_quantile_values(rows, cols, count=None):
+    """Descending singular values at the quantiles (i + 1/2)/m of the
+    Marchenko-Pastur law of a rows x cols N(0, 1/max(rows, cols)) matrix: the
+    deterministic 'typical' bulk, eigenvalues of the Gram in
+    [(1 - sqrt c)^2, (1 + sqrt c)^2] with c = m / n."""
+    import numpy as np
+    n, m = max(rows, cols), min(rows, cols)
+    c = m / n
+    a, b = (1 - math.sqrt(c)) ** 2, (1 + math.sqrt(c)) ** 2
+    # substitution lambda = a + (b - a) sin^2(t) removes the edge singularities
+    t = np.linspace(0.0, math.pi / 2, 200001)
+    lam = a + (b - a) * np.sin(t) ** 2
+    dlam = 2 * (b - a) * np.sin(t) * np.cos(t)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        dens = np.sqrt(np.maximum((b - lam) * (lam - a), 0.0)) / (2 * math.pi * c * lam)
+    w = np.nan_to_num(dens * dlam)
+    cdf = np.concatenate([[0.0], np.cumsum(0.5 * (w[1:] + w[:-1]) * np.diff(t))])
+    cdf /= cdf[-1]
+    q = (np.arange(m) + 0.5) / m
+    ev = np.interp(q, cdf, lam)[::-1]
+    s = np.sqrt(np.maximum(ev, 0.0))
+    return s if count is None else s[:count]
+
+
+def spiked_batch(batch, rows, cols, seed, n_spikes=8, hi=50.0, lo=10.0, device="cpu",
+                 dtype=torch.float32, unspiked=()):
+    """A (batch, rows, cols) stack of synthetic momenta generated on `device`:
+    Haar singular vectors (QR of Gaussians, fp32), the Marchenko-Pastur quantile
+    bulk, and n_spikes values beta*logspace(hi..lo) on top (beta = the bulk's top
+    value).  Matrices whose index is in `unspiked` keep the pure bulk."""
+    import numpy as np
+    gen = _gen(seed, device)
+    m = min(rows, cols)
+    U, _ = torch.linalg.qr(torch.randn(batch, rows, m, generator=gen, device=device))
+    V, _ = torch.linalg.qr(torch.randn(batch, cols, m, generator=gen, device=device))
+    bulk = mp_quantile_values(rows, cols)
+    beta = float(bulk[0])
+    s = np.tile(bulk, (batch, 1))
+    if n_spikes:
+        spikes = beta * np.logspace(math.log10(hi), math.log10(lo), n_spikes)
+        for i in range(batch):
+            if i not in unspiked:
+                s[i, :n_spikes] = spikes
+                s[i, n_spikes:] = bulk[: m - n_spikes]
+    sv = torch.from_numpy(s).to(device=device, dtype=torch.float32)
+    return ((U * sv[:, None, :]) @ V.mT).to(dtype)
