@@ -95,6 +95,20 @@ int dmh_rmfro_clip(dmh_stream_t stream, const float* A, const float* Omega, int 
                    int qr_passes, void* X0, int out_bf16, long long* k, float* d, void* ws,
                    size_t ws_bytes);
 
+/* Fused deflated polar factor: the front-end above followed by the bf16 chain
+ * (tall convention, no entry scaling) over `steps` (a, b, c) triples, i.e. what
+ * muon.py:298 BATCHED_CLIP(out_dtype=bf16) followed by muon.py:310-312 _iterate
+ * computes for one shape group.  X0 is written straight into the chain's packed
+ * operands instead of a separate tensor.  out: (batch, n, m) bf16; k, d as for
+ * dmh_rmfro_clip.  Workspace: dmh_deflated_polar_workspace_size.
+ * chain_event: optional hipEvent_t recorded on `stream` between the front-end and
+ * the chain (phase timing); NULL for none. */
+int dmh_deflated_polar_workspace_size(int batch, int n, int m, int r, size_t* bytes);
+int dmh_deflated_polar(dmh_stream_t stream, const float* A, const float* Omega, int batch, int n,
+                       int m, int r, int kw, float ratio, float thresh, float pad, int niter,
+                       int qr_passes, const double* coeffs, int steps, void* out, long long* k,
+                       float* d, void* ws, size_t ws_bytes, void* chain_event);
+
 #ifdef __cplusplus
 }
 #endif

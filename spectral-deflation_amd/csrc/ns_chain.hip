@@ -26,6 +26,7 @@
 // accumulator instead, which keeps A*A symmetric and lets K2 skip half its
 // tiles.)
 #include "common.h"
+#include "ns_chain.h"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -43,21 +44,24 @@ void set_error(const char* fmt, ...) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA GEMM tile: 256 x 256 output per workgroup, 4 waves of 128 x 128, K step 64.
+// MFMA GEMM tile: 256 x 256 output per workgroup, 4 waves of 128 x 128, K step 32,
+// a 4-stage LDS ring (three K steps of loads in flight while one is consumed).
 //
 // Operand tiles go global -> LDS with the gfx950 direct-to-LDS load
 // (global_load_lds_dwordx4: lane L of a wave writes 16 bytes at base + 16 L, no
-// VGPR round trip), two stages.  An LDS row is 64 bf16 = 128 B = 8 chunks of
-// 16 B; chunk c of row r sits in slot c ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1),
-// which makes the 16-byte fragment reads of 8 (or 16) consecutive rows hit
-// distinct banks.  The swizzle is applied by choosing, for each lane, which
-// global chunk it fetches into its fixed LDS slot.
+// VGPR round trip).  An LDS row is 32 bf16 = 64 B = 4 chunks of 16 B; chunk c of
+// row r sits in slot c ^ swz(r), swz(r) = (r >> 1) & 3, so the 16-byte fragment
+// reads of 8 consecutive rows hit distinct banks.  The swizzle is applied by
+// choosing, for each lane, which global chunk it fetches into its fixed LDS slot.
 // ---------------------------------------------------------------------------
-constexpr int TILE = 256;
-constexpr int TK = 64;
+constexpr int TILE = CHAIN_TILE;
+constexpr int TK = 32;
+constexpr int NSTAGE = 4;
 constexpr int ROWB = TK * 2;                 // bytes per LDS row
-constexpr int OPB = TILE * ROWB;             // bytes per operand tile (32 KB)
+constexpr int OPB = TILE * ROWB;             // bytes per operand tile (16 KB)
+constexpr int STAGEB = 2 * OPB;              // P + Q
 constexpr int GEMM_THREADS = 256;
+static_assert(NSTAGE * STAGEB == 128 * 1024, "LDS ring must equal the epilogue tile");
 
 enum { EPI_STORE = 0, EPI_POLY = 1, EPI_AXPY = 2 };
 
@@ -92,14 +96,26 @@ __device__ __forceinline__ void decode_tile(const GemmArgs& g, int lid, int& b, 
   }
 }
 
-__device__ __forceinline__ int lds_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Workgroup barrier for the LDS ring.  Every wave has already waited (vmcnt) for
+// its own direct-to-LDS loads of the stage about to be read, and its fragment
+// reads of the stage about to be refilled have been consumed by its MFMAs, so the
+// barrier needs no memory fence: __syncthreads() would make the compiler drain
+// all outstanding loads (vmcnt(0)), i.e. the whole prefetch ring, at every step.
+// The empty asm statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 template <int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_nt_bf16(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * OPB];   // [stage][operand]
+  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * STAGEB];
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   int b, ti, tj;
@@ -113,14 +129,14 @@ void gemm_nt_bf16(GemmArgs g) {
   const bf16* P = g.P + (long long)b * g.p_bs + (long long)(ti * TILE) * g.p_ld;
   const bf16* Q = g.Q + (long long)b * g.q_bs + (long long)(tj * TILE) * g.q_ld;
 
-  // Loader: wave w, instruction q covers tile rows 64w + 8q .. +7; lane L fills
-  // slot L & 7 of row 64w + 8q + (L >> 3) with the global chunk slot ^ swz(row).
-  const int lrow0 = 64 * wave + (lane >> 3);
-  const int lslot = lane & 7;
-  int goffP[8], goffQ[8];   // element offsets within the tile (32-bit)
+  // Loader: wave w, instruction q covers tile rows 64w + 16q .. +15; lane L fills
+  // slot L & 3 of row 64w + 16q + (L >> 2) with the global chunk slot ^ swz(row).
+  const int lrow0 = 64 * wave + (lane >> 2);
+  const int lslot = lane & 3;
+  int goffP[4], goffQ[4];   // element offsets within the tile (32-bit)
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int r = lrow0 + 8 * q;
+  for (int q = 0; q < 4; ++q) {
+    const int r = lrow0 + 16 * q;
     const int c = lslot ^ lds_swz(r);
     goffP[q] = r * g.p_ld + c * 8;
     goffQ[q] = r * g.q_ld + c * 8;
@@ -129,13 +145,13 @@ void gemm_nt_bf16(GemmArgs g) {
 
 #define DMH_GLOAD(k0, st)                                                              \
   do {                                                                                 \
-    char* dP = lds_wave + (st) * 2 * OPB;                                              \
+    char* dP = lds_wave + (st) * STAGEB;                                               \
     char* dQ = dP + OPB;                                                               \
-    _Pragma("unroll") for (int q = 0; q < 8; ++q) {                                    \
+    _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                    \
       __builtin_amdgcn_global_load_lds((const void*)(P + (k0) + goffP[q]),             \
-                                       (lds_ptr_t)(dP + q * 8 * ROWB), 16, 0, 0);      \
+                                       (lds_ptr_t)(dP + q * 16 * ROWB), 16, 0, 0);     \
       __builtin_amdgcn_global_load_lds((const void*)(Q + (k0) + goffQ[q]),             \
-                                       (lds_ptr_t)(dQ + q * 8 * ROWB), 16, 0, 0);      \
+                                       (lds_ptr_t)(dQ + q * 16 * ROWB), 16, 0, 0);     \
     }                                                                                  \
   } while (0)
 
@@ -153,109 +169,165 @@ void gemm_nt_bf16(GemmArgs g) {
   // byte offsets of this lane's fragment rows (row 32i + r32 of the wave's half)
   const int fP = (128 * wm + r32) * ROWB;
   const int fQ = OPB + (128 * wn + r32) * ROWB;
-  int fchunk[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) fchunk[s] = ((2 * s + hi) ^ sw) * 16;
+  const int fch0 = ((0 + hi) ^ sw) * 16, fch1 = ((2 + hi) ^ sw) * 16;
 
   const int nk = g.K / TK;
-  DMH_GLOAD(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  // prologue: stages 0 .. NSTAGE-2 in flight; wait for stage 0
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p)
+    if (p < nk) DMH_GLOAD(p * TK, p);
+  if (nk >= 3) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (nk == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  ring_barrier();
 
   for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < nk) DMH_GLOAD((kt + 1) * TK, st ^ 1);
-    const char* base = smem + st * 2 * OPB;
+    const int st = kt & (NSTAGE - 1);
+    const int pre = kt + NSTAGE - 1;
+    if (pre < nk) DMH_GLOAD(pre * TK, pre & (NSTAGE - 1));
+    const char* base = smem + st * STAGEB;
     bf16x8 pf[2][4], qf[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pf[0][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fchunk[0]);
-      qf[0][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fchunk[0]);
+      pf[0][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fch0);
+      qf[0][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fch0);
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int cur = s & 1;
-      if (s + 1 < 4) {
+    for (int i = 0; i < 4; ++i) {
+      pf[1][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fch1);
+      qf[1][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fch1);
+    }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pf[cur ^ 1][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fchunk[s + 1]);
-          qf[cur ^ 1][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fchunk[s + 1]);
-        }
-      }
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[cur][j], pf[cur][i], acc[i][j],
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[s][j], pf[s][i], acc[i][j],
                                                               0, 0, 0);
-    }
-    // Schedule: next-stage loads first, the first fragments, then each k16
-    // step's 16 MFMAs with the 8 fragment reads of the next step issued early.
-    __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);   // VMEM (direct-to-LDS loads)
+    // Schedule: the prefetch loads, the step-0 fragments, then step-1 fragment
+    // reads issued early among the step-0 MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);    // VMEM (direct-to-LDS loads)
     __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS read: step-0 fragments
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
+    for (int x = 0; x < 4; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    __builtin_amdgcn_sched_group_barrier(0x008, 28, 0);
+    // stage kt+1 must be complete; the loads issued after it are those of the
+    // younger stages kt+2 and kt+3 that exist (8 per stage per wave), and loads
+    // retire in issue order
+    if (kt + 3 < nk) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (kt + 2 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    ring_barrier();
   }
 #undef DMH_GLOAD
 
   // ---- epilogue -------------------------------------------------------------
-  // acc[i][j][4g+q] holds C[i0 + (lane&31)][j0 + 8g + 4(lane>>5) + q]
-  const bool diag = g.sym && ti == tj;
-  const bool mirror = g.sym && ti != tj;
+  // The 256x256 output tile is staged through LDS as bf16 (the whole 128 KB),
+  // so both output layouts leave in 16-byte coalesced stores.
+  //   phase 1  acc -> LDS: v = bf16(acc) (bf16(c * acc) for POLY)
+  //   phase 2  row-major pass: epilogue (aux read in 16 B), store C[i][j]
+  //   phase 3  transposed pass: 8 rows x 4 columns per step, transposed in
+  //            registers, store C^T[j][i]
+  // LDS element (i, j) of the tile sits at byte i*512 + 16*((j>>3) ^ swz(i)) + 2*(j&7);
+  // swz(i) = ((i>>3)&3) | ((((i&7) ^ (i>>5)) & 7) << 2) keeps 32 consecutive rows (phase
+  // 1) and rows 8 apart (phase 3) on distinct 16-byte slots.
+  // acc[i][j][4g+q] holds C[i0 + (lane&31)][j0 + 8g + 4(lane>>5) + q].
+  __syncthreads();
+  char* const cs = smem;
+  auto cswz = [](int i) { return ((i >> 3) & 3) | ((((i & 7) ^ (i >> 5)) & 7) << 2); };
+  auto caddr = [&](int i, int j) { return i * 512 + 16 * ((j >> 3) ^ cswz(i)) + 2 * (j & 7); };
 #pragma unroll
   for (int bi = 0; bi < 4; ++bi) {
-    const int i = ti * TILE + 128 * wm + 32 * bi + r32;
+    const int il = 128 * wm + 32 * bi + r32;
 #pragma unroll
     for (int bj = 0; bj < 4; ++bj) {
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const int j0 = tj * TILE + 128 * wn + 32 * bj + 8 * gq + 4 * (lane >> 5);
-        float v[4];
+        const int jl = 128 * wn + 32 * bj + 8 * gq + 4 * (lane >> 5);
+        bf16x4 o;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = acc[bi][bj][4 * gq + q];
-        bf16 o[4];
-        if (EPI == EPI_STORE) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) o[q] = f2bf(v[q]);
-        } else {
-          const bf16* ap = g.aux + (long long)b * g.aux_bs + (long long)i * g.aux_ld + j0;
-          const bf16x4 av = *(const bf16x4*)ap;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (EPI == EPI_POLY)
-              o[q] = f2bf(g.alpha * bf2f(av[q]) + bf2f(f2bf(g.beta * v[q])));
-            else
-              o[q] = f2bf(g.alpha * bf2f(av[q]) + bf2f(f2bf(v[q])));
-          }
+        for (int q = 0; q < 4; ++q) {
+          const float v = acc[bi][bj][4 * gq + q];
+          o[q] = f2bf(EPI == EPI_POLY ? g.beta * v : v);
         }
-        if (i >= g.valid_i) continue;
-        if (g.out) {
-          bf16* op = g.out + (long long)b * g.out_bs + (long long)i * g.out_ld + j0;
-          if (!diag && j0 + 3 < g.valid_j && (g.out_ld & 3) == 0) {
-            bf16x4 ov = {o[0], o[1], o[2], o[3]};
-            *(bf16x4*)op = ov;
-          } else {
+        *(bf16x4*)(cs + caddr(il, jl)) = o;
+      }
+    }
+  }
+  __syncthreads();
+  const bool diag = g.sym && ti == tj;
+  if (diag) {
+    // exact symmetry: the lower triangle of a diagonal tile takes the upper one's values
+    for (int e = tid; e < TILE * TILE; e += GEMM_THREADS) {
+      const int i = e >> 8, j = e & 255;
+      if (i > j) *(bf16*)(cs + caddr(i, j)) = *(const bf16*)(cs + caddr(j, i));
+    }
+    __syncthreads();
+  }
+  const int gi0 = ti * TILE, gj0 = tj * TILE;
+  const bool need_t = g.outT && (!g.sym || !diag);
+  const bf16* auxb = EPI == EPI_STORE ? nullptr : g.aux + (long long)b * g.aux_bs;
+  bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
+  for (int u = 0; u < 32; ++u) {
+    const int e = tid + GEMM_THREADS * u;
+    const int il = e >> 5, jc = (e & 31) * 8;
+    char* lp = cs + il * 512 + 16 * ((jc >> 3) ^ cswz(il));
+    bf16x8 v = *(const bf16x8*)lp;
+    const int gi = gi0 + il, gj = gj0 + jc;
+    if (EPI != EPI_STORE) {
+      const bf16x8 av = *(const bf16x8*)(auxb + (long long)gi * g.aux_ld + gj);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (j0 + q < g.valid_j && (!diag || i <= j0 + q)) op[q] = o[q];
-          }
-        }
-        if (g.outT && (mirror || diag || !g.sym)) {
-          bf16* tp = g.outT + (long long)b * g.outT_bs + i;
+      for (int q = 0; q < 8; ++q) v[q] = f2bf(g.alpha * bf2f(av[q]) + bf2f(v[q]));
+      if (need_t) *(bf16x8*)lp = v;
+    }
+    if (outb && gi < g.valid_i) {
+      bf16* op = outb + (long long)gi * g.out_ld + gj;
+      if (gj + 7 < g.valid_j && (g.out_ld & 7) == 0) {
+        *(bf16x8*)op = v;
+      } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int j = j0 + q;
-            if (j < g.valid_j && (!diag || i < j)) tp[(long long)j * g.outT_ld] = o[q];
+        for (int q = 0; q < 8; ++q)
+          if (gj + q < g.valid_j) op[q] = v[q];
+      }
+    }
+  }
+  if (!need_t) return;
+  __syncthreads();
+  bf16* outtb = g.outT + (long long)b * g.outT_bs;
+  for (int u = 0; u < 8; ++u) {
+    const int e = tid + GEMM_THREADS * u;
+    const int ic = (e & 31) * 8, jg = (e >> 5) * 4;   // rows ic..ic+7, columns jg..jg+3
+    uint2 r[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r[q] = *(const uint2*)(cs + caddr(ic + q, jg));
+    const int gi = gi0 + ic;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int gj = gj0 + jg + c;
+      // column c of the 8x4 block: halves (c&1) of words (c>>1)
+      uint32_t w[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const uint32_t x0 = (c >> 1) ? r[2 * h].y : r[2 * h].x;
+        const uint32_t x1 = (c >> 1) ? r[2 * h + 1].y : r[2 * h + 1].x;
+        const uint32_t lo = (c & 1) ? (x0 >> 16) : (x0 & 0xffffu);
+        const uint32_t hi = (c & 1) ? (x1 & 0xffff0000u) : (x1 << 16);
+        w[h] = lo | hi;
+      }
+      if (gj >= g.valid_j) continue;
+      bf16* tp = outtb + (long long)gj * g.outT_ld + gi;
+      if (gi + 7 < g.valid_i && (g.outT_ld & 7) == 0) {
+        *(uint4*)tp = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          if (gi + q < g.valid_i) {
+            const uint16_t bits = (uint16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xffffu);
+            tp[q] = __builtin_bit_cast(bf16, bits);
           }
         }
       }
@@ -362,11 +434,7 @@ __global__ __launch_bounds__(256) void copy_out(const bf16* T, int np, int mp, i
   }
 }
 
-struct ChainDims {
-  int n, m, np, mp;
-};
-
-static ChainDims chain_dims(int rows, int cols, int orient_tall) {
+ChainDims chain_dims(int rows, int cols, int orient_tall) {
   ChainDims d;
   d.n = orient_tall ? rows : cols;
   d.m = orient_tall ? cols : rows;
@@ -375,11 +443,21 @@ static ChainDims chain_dims(int rows, int cols, int orient_tall) {
   return d;
 }
 
-static size_t chain_ws_bytes(int batch, const ChainDims& d) {
-  const size_t tw = (size_t)batch * d.np * d.mp * sizeof(bf16);
-  const size_t sq = (size_t)batch * d.mp * d.mp * sizeof(bf16);
+ChainWs chain_ws(void* ws, int batch, const ChainDims& d) {
+  ChainWs w{};
+  const size_t tw = (size_t)batch * d.np * d.mp;
+  const size_t sq = (size_t)batch * d.mp * d.mp;
   const size_t part = (size_t)batch * NORM_CHUNKS * sizeof(double);
-  return 4 * tw + 2 * sq + ((part + 255) / 256) * 256;
+  w.bytes = (4 * tw + 2 * sq) * sizeof(bf16) + ((part + 255) / 256) * 256;
+  if (!ws) return w;
+  w.T0 = (bf16*)ws;
+  w.W0 = w.T0 + tw;
+  w.T1 = w.W0 + tw;
+  w.W1 = w.T1 + tw;
+  w.A = w.W1 + tw;
+  w.B = w.A + sq;
+  w.partials = (double*)(w.B + sq);
+  return w;
 }
 
 template <int EPI>
@@ -395,73 +473,19 @@ static int launch_gemm(const GemmArgs& g, int batch, hipStream_t stream, const c
   return DMH_OK;
 }
 
-}  // namespace dmh
-
-using namespace dmh;
-
-extern "C" {
-
-const char* dmh_last_error(void) { return g_err; }
-
-int dmh_ns_workspace_size(int batch, int rows, int cols, int orient_tall, size_t* bytes) {
-  if (batch < 0 || rows <= 0 || cols <= 0 || !bytes) {
-    set_error("dmh_ns_workspace_size: bad arguments");
-    return DMH_EINVAL;
-  }
-  *bytes = chain_ws_bytes(batch, chain_dims(rows, cols, orient_tall));
-  return DMH_OK;
-}
-
-int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int rows, int cols,
-                 long long x_bstride, long long x_rstride, long long x_cstride, void* out,
-                 int orient_tall, int entry_mode, const double* coeffs, int steps, void* ws,
-                 size_t ws_bytes) {
-  if (batch == 0) return DMH_OK;
-  if (!x || !out || batch < 0 || rows <= 0 || cols <= 0 || steps < 0 ||
-      (steps > 0 && !coeffs) || (x_dtype != 0 && x_dtype != 1) || entry_mode < 0 ||
-      entry_mode > 2) {
-    set_error("dmh_ns_chain: bad arguments (batch=%d rows=%d cols=%d steps=%d dtype=%d mode=%d)",
-              batch, rows, cols, steps, x_dtype, entry_mode);
-    return DMH_EINVAL;
-  }
-  const ChainDims d = chain_dims(rows, cols, orient_tall);
-  const size_t need = chain_ws_bytes(batch, d);
-  if (!ws || ws_bytes < need) {
-    set_error("dmh_ns_chain: workspace %zu < %zu bytes", ws_bytes, need);
-    return DMH_EWORKSPACE;
-  }
-  const size_t tw = (size_t)batch * d.np * d.mp;
-  const size_t sq = (size_t)batch * d.mp * d.mp;
-  bf16* T0 = (bf16*)ws;
-  bf16* W0 = T0 + tw;
-  bf16* T1 = W0 + tw;
-  bf16* W1 = T1 + tw;
-  bf16* Am = W1 + tw;
-  bf16* Bm = Am + sq;
-  double* partials = (double*)(Bm + sq);
-
-  InView v{x, x_dtype, x_bstride, x_rstride, x_cstride, rows, cols};
-  if (entry_mode) {
-    hipLaunchKernelGGL(entry_norm_partials, dim3(NORM_CHUNKS, batch), dim3(256), 0, stream, v,
-                       partials);
-    DMH_CHECK_LAUNCH("entry_norm_partials");
-  }
-  hipLaunchKernelGGL(entry_pack, dim3(d.mp / 64, d.np / 64, batch), dim3(256), 0, stream, v,
-                     orient_tall, entry_mode, partials, d.n, d.m, d.np, d.mp, T0, W0);
-  DMH_CHECK_LAUNCH("entry_pack");
-
-  bf16* outp = (bf16*)out;
+int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const ChainDims& d,
+                     int orient_tall, const double* coeffs, int steps, bf16* outp) {
   if (steps == 0) {
     const long long total = (long long)d.n * d.m;
     const int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
-    hipLaunchKernelGGL(copy_out, dim3(blocks, batch), dim3(256), 0, stream, T0, d.np, d.mp, d.n,
-                       d.m, orient_tall, outp);
+    hipLaunchKernelGGL(copy_out, dim3(blocks, batch), dim3(256), 0, stream, w.T0, d.np, d.mp,
+                       d.n, d.m, orient_tall, outp);
     DMH_CHECK_LAUNCH("copy_out");
     return DMH_OK;
   }
-
   const int tm = d.mp / TILE, tn = d.np / TILE;
-  bf16 *Tc = T0, *Wc = W0, *Tn = T1, *Wn = W1;
+  bf16 *Tc = w.T0, *Wc = w.W0, *Tn = w.T1, *Wn = w.W1;
+  bf16 *Am = w.A, *Bm = w.B;
   for (int it = 0; it < steps; ++it) {
     const float a = (float)coeffs[3 * it + 0];
     const float bcoef = (float)coeffs[3 * it + 1];
@@ -509,6 +533,53 @@ int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int 
     t = Wc; Wc = Wn; Wn = t;
   }
   return DMH_OK;
+}
+
+}  // namespace dmh
+
+using namespace dmh;
+
+extern "C" {
+
+const char* dmh_last_error(void) { return g_err; }
+
+int dmh_ns_workspace_size(int batch, int rows, int cols, int orient_tall, size_t* bytes) {
+  if (batch < 0 || rows <= 0 || cols <= 0 || !bytes) {
+    set_error("dmh_ns_workspace_size: bad arguments");
+    return DMH_EINVAL;
+  }
+  *bytes = chain_ws(nullptr, batch, chain_dims(rows, cols, orient_tall)).bytes;
+  return DMH_OK;
+}
+
+int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int rows, int cols,
+                 long long x_bstride, long long x_rstride, long long x_cstride, void* out,
+                 int orient_tall, int entry_mode, const double* coeffs, int steps, void* ws,
+                 size_t ws_bytes) {
+  if (batch == 0) return DMH_OK;
+  if (!x || !out || batch < 0 || rows <= 0 || cols <= 0 || steps < 0 ||
+      (steps > 0 && !coeffs) || (x_dtype != 0 && x_dtype != 1) || entry_mode < 0 ||
+      entry_mode > 2) {
+    set_error("dmh_ns_chain: bad arguments (batch=%d rows=%d cols=%d steps=%d dtype=%d mode=%d)",
+              batch, rows, cols, steps, x_dtype, entry_mode);
+    return DMH_EINVAL;
+  }
+  const ChainDims d = chain_dims(rows, cols, orient_tall);
+  const ChainWs w = chain_ws(ws, batch, d);
+  if (!ws || ws_bytes < w.bytes) {
+    set_error("dmh_ns_chain: workspace %zu < %zu bytes", ws_bytes, w.bytes);
+    return DMH_EWORKSPACE;
+  }
+  InView v{x, x_dtype, x_bstride, x_rstride, x_cstride, rows, cols};
+  if (entry_mode) {
+    hipLaunchKernelGGL(entry_norm_partials, dim3(NORM_CHUNKS, batch), dim3(256), 0, stream, v,
+                       w.partials);
+    DMH_CHECK_LAUNCH("entry_norm_partials");
+  }
+  hipLaunchKernelGGL(entry_pack, dim3(d.mp / 64, d.np / 64, batch), dim3(256), 0, stream, v,
+                     orient_tall, entry_mode, w.partials, d.n, d.m, d.np, d.mp, w.T0, w.W0);
+  DMH_CHECK_LAUNCH("entry_pack");
+  return chain_run_packed(stream, w, batch, d, orient_tall, coeffs, steps, (bf16*)out);
 }
 
 }  // extern "C"

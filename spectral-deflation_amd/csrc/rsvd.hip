@@ -15,10 +15,11 @@
 //   right_mult          C = Y M       (rows x RP) x (RP x RP)
 //   eig_gate            Jacobi eigen-decomposition of Bp Bp^T in LDS (fp64) -> s, Ub;
 //                       the deflation gate and the per-column deflate/restore weights
-//   deflate_norm        partial ||A - U diag(s h) V^T||_F^2 (fp64)
-//   finish_norm         d = ||W||_F + 1e-7
-//   deflate_restore     X0 = W / d + U diag(h / pad) V^T  -> bf16 or fp32
+//                       and d = ||A - U diag(s h) V^T||_F + 1e-7 from r x r quantities
+//   deflate_restore     X0 = W / d + U diag(h / pad) V^T  -> bf16 / fp32, or straight
+//                       into the NS chain's packed operands (fused deflated polar)
 #include "common.h"
+#include "ns_chain.h"
 
 #include <math.h>
 
@@ -45,7 +46,8 @@ template <int MODE>
 __global__ __launch_bounds__(256) void skinny_gemm(const float* __restrict__ A, int n, int m,
                                                    long long a_bs, const float* __restrict__ X,
                                                    int ld_x, int xcols, long long x_bs,
-                                                   float* __restrict__ C, long long c_bs) {
+                                                   float* __restrict__ C, long long c_bs,
+                                                   double* __restrict__ asq) {
   constexpr int APITCH = MODE == SG_ROWSTREAM ? SG_K + 1 : SG_ROWS;
   constexpr int AROWS = MODE == SG_ROWSTREAM ? SG_ROWS : SG_K;
   __shared__ float As[AROWS * APITCH];
@@ -93,6 +95,7 @@ __global__ __launch_bounds__(256) void skinny_gemm(const float* __restrict__ A, 
   } while (0)
 
   const int nchunks = (K + SG_K - 1) / SG_K;
+  double sq = 0.0;   // sum of squares of this thread's A elements (asq != nullptr)
   DMH_SG_LOAD(0);
   const int l32 = lane & 31, lh = lane >> 5;
   const int wrow = wave * 32;   // this wave's 32 output rows within the tile
@@ -106,6 +109,12 @@ __global__ __launch_bounds__(256) void skinny_gemm(const float* __restrict__ A, 
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) Xs[tid + 256 * u] = rx[u];
+    if (MODE == SG_ROWSTREAM && asq) {
+      float f = 0.f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) f = fmaf(ra[u], ra[u], f);
+      sq += (double)f;
+    }
     __syncthreads();
     if (ch + 1 < nchunks) DMH_SG_LOAD((ch + 1) * SG_K);
 #pragma unroll
@@ -127,6 +136,17 @@ __global__ __launch_bounds__(256) void skinny_gemm(const float* __restrict__ A, 
       C[(long long)row * RP + l32] = acc0[e];
       C[(long long)row * RP + 32 + l32] = acc1[e];
     }
+  }
+  if (MODE == SG_ROWSTREAM && asq) {
+    __syncthreads();
+    double* red = (double*)As;   // 256 doubles fit in the A tile
+    red[tid] = sq;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+      if (tid < w) red[tid] += red[tid + w];
+      __syncthreads();
+    }
+    if (tid == 0) asq[(long long)b * gridDim.x + blockIdx.x] = red[0];
   }
 #undef DMH_SG_LOAD
 }
@@ -191,78 +211,122 @@ __device__ void sum_gram_partials(const double* part, int b, int r, double (*G)[
 // matrix.  A non-positive or non-finite pivot marks the matrix degenerate: M is
 // then zero, so everything downstream of it is zero and the gate declines.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void chol_inv(const double* __restrict__ part, int r,
-                                                float* __restrict__ M, int* __restrict__ degen) {
-  __shared__ double G[RP][RP + 1];
-  __shared__ double Li[RP][RP + 1];
-  __shared__ int fail;
-  const int b = blockIdx.x, tid = threadIdx.x;
-  sum_gram_partials(part, b, r, G);
-  if (tid == 0) fail = 0;
-  __syncthreads();
-  for (int k = 0; k < r; ++k) {
-    if (tid == 0) {
-      const double d = G[k][k];
-      if (!(d > 0.0) || !isfinite(d)) fail = 1;
-      G[k][k] = sqrt(d > 0.0 ? d : 1.0);
-    }
-    __syncthreads();
-    const double lkk = G[k][k];
-    for (int i = k + 1 + tid; i < r; i += blockDim.x) G[i][k] /= lkk;
-    __syncthreads();
-    const int w = r - k - 1;
-    for (int e = tid; e < w * w; e += blockDim.x) {
-      const int i = k + 1 + e / w, j = k + 1 + e % w;
-      if (j <= i) G[i][j] -= G[i][k] * G[j][k];
-    }
-    __syncthreads();
-  }
-  // Li = L^-1 (lower): column j by forward substitution
-  if (tid < r) {
-    const int j = tid;
-    for (int i = 0; i < r; ++i) {
-      double s = (i == j) ? 1.0 : 0.0;
-      for (int t = j; t < i; ++t) s -= G[i][t] * Li[t][j];
-      Li[i][j] = i < j ? 0.0 : s / G[i][i];
-    }
-  }
-  __syncthreads();
-  // M = L^-T: M[a][c] = Li[c][a]
-  float* Mb = M + (long long)b * RP * RP;
-  for (int e = tid; e < RP * RP; e += blockDim.x) {
-    const int a = e / RP, c = e % RP;
-    Mb[e] = (!fail && a < r && c < r) ? (float)Li[c][a] : 0.f;
-  }
-  if (tid == 0 && degen) degen[b] |= fail;
+__device__ __forceinline__ double lane_val(double v, int lane) {
+  const long long bits = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(bits & 0xffffffffLL), lane);
+  const int hi = __builtin_amdgcn_readlane((int)(bits >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// C (rows x RP) = Y (rows x RP) * M (RP x RP), per matrix
+// One wavefront per matrix, everything in registers: lane l holds row l of the
+// (identity-padded) Gram, the factorization and the inversion are fully unrolled
+// over the 64 x 64 problem, and values of other rows arrive by readlane.
+__global__ __launch_bounds__(64) void chol_inv(const double* __restrict__ part, int r,
+                                               float* __restrict__ M, int* __restrict__ degen) {
+  const int b = blockIdx.x, l = threadIdx.x;
+  __shared__ double Ls[RP][RP + 1];
+  {
+    const double* pb = part + (long long)b * GRAM_CHUNKS * RP * RP;
+    for (int e = l; e < RP * RP; e += 64) {
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < GRAM_CHUNKS; ++c) acc += pb[(long long)c * RP * RP + e];
+      const int i = e / RP, j = e % RP;
+      Ls[i][j] = (i < r && j < r) ? acc : (i == j ? 1.0 : 0.0);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  double g[RP];
+#pragma unroll
+  for (int j = 0; j < RP; ++j) g[j] = Ls[l][j];
+  // right-looking Cholesky: after step k, g[k] of lane l >= k holds L[l][k]
+  bool fail = false;
+#pragma unroll
+  for (int k = 0; k < RP; ++k) {
+    const double dk = lane_val(g[k], k);
+    fail |= !(dk > 0.0) || !isfinite(dk);
+    const double lkk = sqrt(dk > 0.0 ? dk : 1.0);
+    const double lik = (l > k) ? g[k] / lkk : (l == k ? lkk : 0.0);
+    g[k] = lik;
+#pragma unroll
+    for (int j = k + 1; j < RP; ++j) {
+      const double ljk = lane_val(lik, j);       // L[j][k]
+      if (l >= j) g[j] -= lik * ljk;
+    }
+  }
+  // L to LDS (row l from lane l); then x = column l of L^-1 by forward
+  // substitution, L[i][i] x_i = delta_il - sum_{t<i} L[i][t] x_t (broadcast reads of L)
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < RP; ++j) Ls[l][j] = g[j];
+  __builtin_amdgcn_wave_barrier();
+  double x[RP];
+#pragma unroll
+  for (int i = 0; i < RP; ++i) {
+    double sacc = (i == l) ? 1.0 : 0.0;
+#pragma unroll
+    for (int t = 0; t < i; ++t) sacc -= Ls[i][t] * x[t];
+    x[i] = (i < l) ? 0.0 : sacc / Ls[i][i];
+  }
+  // M = L^-T: M[a][c] = (L^-1)[c][a] = x_c of lane a... lane l holds column l of L^-1,
+  // i.e. row l of M
+  float* Mb = M + (long long)b * RP * RP + (long long)l * RP;
+#pragma unroll
+  for (int c = 0; c < RP; ++c) Mb[c] = (!fail && l < r && c < r) ? (float)x[c] : 0.f;
+  if (l == 0 && degen && fail) degen[b] = 1;
+}
+
+// C (rows x RP) = Y (rows x RP) * M (RP x RP), per matrix; 64 rows per workgroup,
+// a 4 x 4 output block per thread.
 __global__ __launch_bounds__(256) void right_mult(const float* __restrict__ Y, int rows,
                                                   long long y_bs, const float* __restrict__ M,
                                                   float* __restrict__ C, long long c_bs) {
-  __shared__ float Ms[RP * RP];
-  __shared__ float Ys[64][RP + 1];
+  __shared__ __attribute__((aligned(16))) float Ms[RP * RP];
+  __shared__ __attribute__((aligned(16))) float Ys[64][RP + 4];
   const int b = blockIdx.y, r0 = blockIdx.x * 64, tid = threadIdx.x;
   const float* Mb = M + (long long)b * RP * RP;
-  for (int e = tid; e < RP * RP; e += 256) Ms[e] = Mb[e];
-  for (int e = tid; e < 64 * RP; e += 256) {
-    const int row = r0 + e / RP;
-    Ys[e / RP][e % RP] = row < rows ? Y[(long long)b * y_bs + (long long)row * RP + e % RP] : 0.f;
+  const float* Yb = Y + (long long)b * y_bs;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = tid + 256 * u;              // float4 index
+    *(float4*)&Ms[4 * e] = *(const float4*)&Mb[4 * e];
+    const int rr = e >> 4, c4 = (e & 15) * 4;
+    const int row = r0 + rr;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < rows) v = *(const float4*)&Yb[(long long)row * RP + c4];
+    *(float4*)&Ys[rr][c4] = v;
   }
   __syncthreads();
-  const int col = tid & 63, rq = tid >> 6;
-  for (int rr = rq; rr < 64; rr += 4) {
-    float s = 0.f;
-#pragma unroll 16
-    for (int a = 0; a < RP; ++a) s = fmaf(Ys[rr][a], Ms[a * RP + col], s);
-    const int row = r0 + rr;
-    if (row < rows) C[(long long)b * c_bs + (long long)row * RP + col] = s;
+  const int ty = tid >> 4, tx = tid & 15;
+  float acc[4][4] = {};
+#pragma unroll 8
+  for (int a2 = 0; a2 < RP; ++a2) {
+    const float4 m = *(const float4*)&Ms[a2 * RP + 4 * tx];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float y = Ys[4 * ty + i][a2];
+      acc[i][0] = fmaf(y, m.x, acc[i][0]);
+      acc[i][1] = fmaf(y, m.y, acc[i][1]);
+      acc[i][2] = fmaf(y, m.z, acc[i][2]);
+      acc[i][3] = fmaf(y, m.w, acc[i][3]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = r0 + 4 * ty + i;
+    if (row < rows)
+      *(float4*)&C[(long long)b * c_bs + (long long)row * RP + 4 * tx] =
+          make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Eigen-decomposition of H = Bp Bp^T (r x r, fp64) by cyclic Jacobi with the
-// round-robin ordering (r/2 disjoint rotations per round), then the gate.
+// round-robin ordering (r/2 disjoint rotations per round), one wavefront per
+// matrix: the wave works wave-synchronously on H and V in LDS (LDS accesses of a
+// wave complete in order), so no workgroup barriers are needed.  A rotation is
+// skipped when |h_pq| <= 1e-12 sqrt(h_pp h_qq) or |h_pq| <= 1e-15 trace(H); a
+// sweep without rotations ends the iteration.  Then the gate.
 // Outputs per matrix: s (descending, fp32), Ub (RP x RP: column t = eigenvector
 // of s_t), UbS = Ub diag(1/s) (for V = Bp^T Ub / s), the deflation width k and
 // the deflate / restore weights cw[t] = s_t h_t, cr[t] = h_t / pad.
@@ -272,252 +336,322 @@ struct GateParams {
   float ratio, thresh, pad;
 };
 
-__global__ __launch_bounds__(256) void eig_gate(const double* __restrict__ part, GateParams gp,
-                                                const int* __restrict__ degen,
-                                                float* __restrict__ s_out, int s_ld,
-                                                float* __restrict__ Ub, float* __restrict__ UbS,
-                                                long long* __restrict__ k_out,
-                                                int* __restrict__ k_int,
-                                                float* __restrict__ cw, float* __restrict__ cr) {
-  __shared__ double H[RP][RP + 1];
-  __shared__ double V[RP][RP + 1];
-  __shared__ double cs_c[RP / 2], cs_s[RP / 2];
-  __shared__ int pp[RP / 2], qq[RP / 2];
-  __shared__ double red[256];
+constexpr int JP = RP + 1;   // LDS pitch: column walks hit distinct banks
+constexpr int NPAIR = RP / 2;
+
+__device__ __forceinline__ double bcast_lane(double v, int lane) {
+  const long long bits = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(bits & 0xffffffffLL), lane);
+  const int hi = __builtin_amdgcn_readlane((int)(bits >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+__global__ __launch_bounds__(64) void eig_gate(const double* __restrict__ part, GateParams gp,
+                                               const int* __restrict__ degen,
+                                               float* __restrict__ s_out, int s_ld,
+                                               float* __restrict__ Ub, float* __restrict__ UbS,
+                                               long long* __restrict__ k_out,
+                                               int* __restrict__ k_int,
+                                               float* __restrict__ cw, float* __restrict__ cr,
+                                               const double* __restrict__ qpart,
+                                               const double* __restrict__ asq, int asq_n,
+                                               float* __restrict__ d_out) {
+  // The whole RP x RP problem is rotated (rows/columns >= r are zero and never
+  // rotate), so the pair schedule is a compile-time 32 pairs x 63 rounds.
+  __shared__ double H[RP * JP];
+  __shared__ float V[RP * JP];        // eigenvectors (accumulated rotations), fp32
   __shared__ int order[RP];
   __shared__ float sv[RP];
-  const int b = blockIdx.x, tid = threadIdx.x;
+  const int b = blockIdx.x, l = threadIdx.x;
   const int r = gp.r;
-  sum_gram_partials(part, b, r, H);
-  for (int e = tid; e < RP * RP; e += 256) V[e / RP][e % RP] = (e / RP == e % RP) ? 1.0 : 0.0;
-  __syncthreads();
-
-  const int rn = (r + 1) & ~1;   // even count for the round-robin (index r is a dummy)
-  const int npairs = rn / 2;
-  for (int sweep = 0; sweep < 30; ++sweep) {
-    // convergence: off-diagonal mass against the diagonal
-    double off = 0.0, dia = 0.0;
-    for (int e = tid; e < r * r; e += 256) {
-      const int i = e / r, j = e % r;
-      const double h = H[i][j];
-      if (i == j) dia += h * h; else off += h * h;
+  {
+    const double* pb = part + (long long)b * GRAM_CHUNKS * RP * RP;
+    for (int e = l; e < RP * RP; e += 64) {
+      const int i = e / RP, j = e % RP;
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < GRAM_CHUNKS; ++c) acc += pb[(long long)c * RP * RP + e];
+      H[i * JP + j] = (i < r && j < r) ? acc : 0.0;
+      V[i * JP + j] = (i == j) ? 1.f : 0.f;
     }
-    red[tid] = off;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) { if (tid < w) red[tid] += red[tid + w]; __syncthreads(); }
-    const double offs = red[0];
-    __syncthreads();
-    red[tid] = dia;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) { if (tid < w) red[tid] += red[tid + w]; __syncthreads(); }
-    const double dias = red[0];
-    __syncthreads();
-    if (offs <= 1e-30 * dias || offs == 0.0) break;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // absolute floor for |h_pq| (trace H = sum of the eigenvalues, invariant): off-
+  // diagonals at rounding level relative to the largest eigenvalue stop rotating,
+  // which guarantees the sweeps end
+  double tr = (l < r) ? fabs(H[l * JP + l]) : 0.0;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) tr += __shfl_xor(tr, o);
+  const double floor_pq = 1e-15 * tr;
 
-    for (int round = 0; round < rn - 1; ++round) {
-      if (tid < npairs) {
-        // round-robin: position 0 fixed, the others rotate
-        auto slot = [&](int x) { return x == 0 ? 0 : 1 + (x - 1 + round) % (rn - 1); };
-        int p = slot(tid), q = slot(rn - 1 - tid);
+  for (int sweep = 0; sweep < 40; ++sweep) {
+    bool rotated = false;
+    for (int rd = 0; rd < RP - 1; ++rd) {
+      // lane t < 32 decides the rotation of pair t (circle method, position 0 fixed)
+      double c = 1.0, sn = 0.0;
+      if (l < NPAIR) {
+        const int x1 = RP - 1 - l;
+        int p = l == 0 ? 0 : 1 + (l - 1 + rd) % (RP - 1);
+        int q = 1 + (x1 - 1 + rd) % (RP - 1);
         if (p > q) { const int t = p; p = q; q = t; }
-        double c = 1.0, s = 0.0;
-        if (q < r) {
-          const double hpq = H[p][q];
-          if (fabs(hpq) > 1e-300) {
-            const double theta = (H[q][q] - H[p][p]) / (2.0 * hpq);
-            const double t = (theta >= 0 ? 1.0 : -1.0) / (fabs(theta) + sqrt(1.0 + theta * theta));
-            c = 1.0 / sqrt(1.0 + t * t);
-            s = t * c;
-          }
+        const double hpq = H[p * JP + q];
+        const double hpp = H[p * JP + p], hqq = H[q * JP + q];
+        if (fabs(hpq) > 1e-12 * sqrt(fabs(hpp * hqq)) && fabs(hpq) > floor_pq) {
+          const double theta = (hqq - hpp) / (2.0 * hpq);
+          const double t = (theta >= 0 ? 1.0 : -1.0) / (fabs(theta) + sqrt(1.0 + theta * theta));
+          c = 1.0 / sqrt(1.0 + t * t);
+          sn = t * c;
         }
-        pp[tid] = p; qq[tid] = q; cs_c[tid] = c; cs_s[tid] = s;
       }
-      __syncthreads();
-      // rows: H <- J^T H
-      for (int e = tid; e < npairs * r; e += 256) {
-        const int pr = e / r, col = e % r;
-        const int p = pp[pr], q = qq[pr];
-        if (q >= r) continue;
-        const double c = cs_c[pr], s = cs_s[pr];
-        const double hp = H[p][col], hq = H[q][col];
-        H[p][col] = c * hp - s * hq;
-        H[q][col] = s * hp + c * hq;
+      if (!__ballot(sn != 0.0)) continue;
+      rotated = true;
+      double cs[NPAIR], ss[NPAIR];
+      int ps[NPAIR], qs[NPAIR];
+#pragma unroll
+      for (int t = 0; t < NPAIR; ++t) {
+        cs[t] = bcast_lane(c, t);
+        ss[t] = bcast_lane(sn, t);
+        const int x1 = RP - 1 - t;
+        int p = t == 0 ? 0 : 1 + (t - 1 + rd) % (RP - 1);
+        int q = 1 + (x1 - 1 + rd) % (RP - 1);
+        ps[t] = p < q ? p : q;
+        qs[t] = p < q ? q : p;
       }
-      __syncthreads();
-      // columns: H <- H J, V <- V J
-      for (int e = tid; e < npairs * r; e += 256) {
-        const int pr = e / r, row = e % r;
-        const int p = pp[pr], q = qq[pr];
-        if (q >= r) continue;
-        const double c = cs_c[pr], s = cs_s[pr];
-        const double hp = H[row][p], hq = H[row][q];
-        H[row][p] = c * hp - s * hq;
-        H[row][q] = s * hp + c * hq;
-        const double vp = V[row][p], vq = V[row][q];
-        V[row][p] = c * vp - s * vq;
-        V[row][q] = s * vp + c * vq;
+      // rows: H <- J^T H  (lane = column); all loads first, then all stores
+      {
+        double hp[NPAIR], hq[NPAIR];
+#pragma unroll
+        for (int t = 0; t < NPAIR; ++t) { hp[t] = H[ps[t] * JP + l]; hq[t] = H[qs[t] * JP + l]; }
+#pragma unroll
+        for (int t = 0; t < NPAIR; ++t) {
+          H[ps[t] * JP + l] = cs[t] * hp[t] - ss[t] * hq[t];
+          H[qs[t] * JP + l] = ss[t] * hp[t] + cs[t] * hq[t];
+        }
       }
-      __syncthreads();
+      __builtin_amdgcn_wave_barrier();
+      // columns: H <- H J, V <- V J  (lane = row)
+      {
+        double hp[NPAIR], hq[NPAIR];
+#pragma unroll
+        for (int t = 0; t < NPAIR; ++t) { hp[t] = H[l * JP + ps[t]]; hq[t] = H[l * JP + qs[t]]; }
+#pragma unroll
+        for (int t = 0; t < NPAIR; ++t) {
+          H[l * JP + ps[t]] = cs[t] * hp[t] - ss[t] * hq[t];
+          H[l * JP + qs[t]] = ss[t] * hp[t] + cs[t] * hq[t];
+        }
+      }
+      {
+        float vp[NPAIR], vq[NPAIR];
+#pragma unroll
+        for (int t = 0; t < NPAIR; ++t) { vp[t] = V[l * JP + ps[t]]; vq[t] = V[l * JP + qs[t]]; }
+#pragma unroll
+        for (int t = 0; t < NPAIR; ++t) {
+          const float cf = (float)cs[t], sf = (float)ss[t];
+          V[l * JP + ps[t]] = cf * vp[t] - sf * vq[t];
+          V[l * JP + qs[t]] = sf * vp[t] + cf * vq[t];
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
     }
+    if (!rotated) break;
   }
   // sort eigenvalues descending (stable rank; NaN ranks last)
-  if (tid < RP) order[tid] = tid;
-  __syncthreads();
-  if (tid < r) {
-    const double li = isnan(H[tid][tid]) ? -INFINITY : H[tid][tid];
+  order[l] = l;
+  __builtin_amdgcn_wave_barrier();
+  if (l < r) {
+    const double li = isnan(H[l * JP + l]) ? -INFINITY : H[l * JP + l];
     int rank = 0;
     for (int j = 0; j < r; ++j) {
-      const double lj = isnan(H[j][j]) ? -INFINITY : H[j][j];
-      rank += (lj > li) || (lj == li && j < tid);
+      const double lj = isnan(H[j * JP + j]) ? -INFINITY : H[j * JP + j];
+      rank += (lj > li) || (lj == li && j < l);
     }
-    order[rank] = tid;
+    order[rank] = l;
   }
-  __syncthreads();
+  __builtin_amdgcn_wave_barrier();
   const bool bad = degen && degen[b];
-  if (tid < RP) {
+  {
     float sval = 0.f;
-    if (tid < r && !bad) {
-      const double l = H[order[tid]][order[tid]];
-      sval = (float)sqrt(l > 0.0 ? l : 0.0);
+    if (l < r && !bad) {
+      const double ev = H[order[l] * JP + order[l]];
+      sval = (float)sqrt(ev > 0.0 ? ev : 0.0);
     }
-    sv[tid] = sval;
+    sv[l] = sval;
   }
-  __syncthreads();
+  __builtin_amdgcn_wave_barrier();
   // gate, fp32 comparisons as torch does them (deflation_batched.py:177-180)
-  __shared__ int s_kk, s_fired;
-  if (tid == 0) {
-    const float s0 = sv[0];
-    const float thr = gp.thresh * s0;
-    int kr = 0;
-    for (int i = 0; i < r; ++i) kr += sv[i] > thr;
-    const bool fired = (sv[gp.kw - 1] < gp.ratio * s0) && kr >= 1 && kr < r;
-    int kk = kr < 1 ? 1 : (kr > r - 1 ? r - 1 : kr);
-    s_kk = kk;
-    s_fired = fired ? 1 : 0;
+  const float s0 = sv[0];
+  const float thr = gp.thresh * s0;
+  const int kr = (int)__popcll(__ballot(l < r && sv[l] > thr));
+  const bool fired = (sv[gp.kw - 1] < gp.ratio * s0) && kr >= 1 && kr < r;
+  const int kk = kr < 1 ? 1 : (kr > r - 1 ? r - 1 : kr);
+  if (l == 0) {
     k_out[b] = fired ? (long long)kk : 0LL;
     k_int[b] = fired ? kk : 0;
   }
-  __syncthreads();
-  const int kk = s_kk, fired = s_fired;
-  if (tid < RP) {
-    if (tid < r) s_out[(long long)b * s_ld + tid] = sv[tid];
-    const float h = (fired && tid < kk) ? 1.f : 0.f;
-    cw[(long long)b * RP + tid] = sv[tid] * h;
-    cr[(long long)b * RP + tid] = h * (1.0f / gp.pad);
-  }
+  if (l < r) s_out[(long long)b * s_ld + l] = sv[l];
+  const float h = (fired && l < kk) ? 1.f : 0.f;
+  cw[(long long)b * RP + l] = sv[l] * h;
+  cr[(long long)b * RP + l] = h * (1.0f / gp.pad);
   float* Ubb = Ub + (long long)b * RP * RP;
   float* UbSb = UbS + (long long)b * RP * RP;
-  for (int e = tid; e < RP * RP; e += 256) {
+  for (int e = l; e < RP * RP; e += 64) {
     const int a = e / RP, t = e % RP;   // row a of Ub, column t (sorted)
     float u = 0.f;
-    if (a < r && t < r && !bad) u = (float)V[a][order[t]];
+    if (a < r && t < r && !bad) u = V[a * JP + order[t]];
     Ubb[e] = u;
     UbSb[e] = sv[t] > 0.f ? u / sv[t] : 0.f;
   }
+  if (!d_out) return;
+  // ||W||_F^2 for W = A - sum_{t<k} s_t U_t V_t^T with U_t = Q Ub_t, V_t = Bp^T Ub_t / s_t:
+  //   <A, U_t V_t^T> = Ub_t^T (Q^T A)(A^T Q) Ub_t / s_t = lambda_t / s_t,
+  //   V_t^T V_t' = delta_tt' lambda_t / s_t^2,  U_t^T U_t = Ub_t^T (Q^T Q) Ub_t = G_t,
+  // so ||W||^2 = ||A||^2 - sum_{t<k} lambda_t (2 - G_t).  Q^T Q is kept (not assumed
+  // to be I): single-pass CholeskyQR in fp32 leaves it ~kappa*eps off the identity,
+  // and the reference's explicit W sees the same Q.
+  double asum = 0.0;
+  for (int i = l; i < asq_n; i += 64) asum += asq[(long long)b * asq_n + i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) asum += __shfl_xor(asum, o);
+  double w2 = asum;
+  if (fired) {
+    const double lam_l = (l < r) ? H[order[l] * JP + order[l]] : 0.0;   // lambda of rank l
+    __builtin_amdgcn_wave_barrier();
+    // reuse H for Q^T Q
+    const double* qb = qpart + (long long)b * GRAM_CHUNKS * RP * RP;
+    for (int e = l; e < RP * RP; e += 64) {
+      const int i = e / RP, j = e % RP;
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < GRAM_CHUNKS; ++c) acc += qb[(long long)c * RP * RP + e];
+      H[i * JP + j] = (i < r && j < r) ? acc : 0.0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    double head = 0.0;
+    for (int t = 0; t < kk; ++t) {
+      const int ct = order[t];
+      double y = 0.0;                       // (Q^T Q Ub_t)_l
+      if (l < r)
+        for (int c = 0; c < r; ++c) y = fma(H[l * JP + c], (double)V[c * JP + ct], y);
+      double gt = (l < r) ? (double)V[l * JP + ct] * y : 0.0;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) gt += __shfl_xor(gt, o);
+      const double lam = __shfl(lam_l, t);
+      head += lam * (2.0 - gt);
+    }
+    w2 = asum - head;
+  }
+  if (l == 0) d_out[b] = (float)sqrt(w2 > 0.0 ? w2 : 0.0) + 1e-7f;
 }
 
 // ---------------------------------------------------------------------------
-// Deflate / restore.  Per 64 x 64 tile of A: W = A - sum_{t<k} U[i][t] cw[t] V[j][t]
+// Restore pass (deflation_batched.py:184-188):
+//   X0 = (A - U diag(s h) V^T) / d + U diag(h / pad) V^T
+//      = A / d - sum_{t<k} U[i][t] (cw_t / d - cr_t) V[j][t]
+// per 64 x 64 tile, rank-k update on VALU (k <= 63), fp32.  Outputs, any subset:
+//   X0   (B, n, m) bf16 or fp32, the API tensor
+//   T, W the NS chain's packed bf16 operands (np x mp and its transpose, zero
+//        outside n x m), so the chain can start without its entry pass
 // ---------------------------------------------------------------------------
-template <bool RESTORE>
-__global__ __launch_bounds__(256) void deflate_tile(
+constexpr int DR_ROWS = 64, DR_COLS = 128;
+
+__global__ __launch_bounds__(256) void deflate_restore(
     const float* __restrict__ A, int n, int m, const float* __restrict__ U,
     const float* __restrict__ V, const int* __restrict__ kvec, const float* __restrict__ cw,
-    const float* __restrict__ cr, double* __restrict__ npart, const float* __restrict__ dvec,
-    void* __restrict__ X0, int out_bf16) {
-  __shared__ float Us[DT][RP + 1];    // U[i][t] (row i of the tile)
-  __shared__ float Vt[RP][DT + 4];    // V[j][t] transposed: Vt[t][j]
-  __shared__ float cws[RP], crs[RP];
-  __shared__ double red[256];
+    const float* __restrict__ cr, const float* __restrict__ dvec, void* __restrict__ X0,
+    int x0_mode /*0 none, 1 bf16, 2 fp32*/, bf16* __restrict__ T, bf16* __restrict__ W, int np,
+    int mp) {
+  __shared__ __attribute__((aligned(16))) float Us[DR_ROWS][RP + 1];   // U[i][t], tile rows
+  __shared__ __attribute__((aligned(16))) float Vt[RP][DR_COLS + 4];   // V[j][t] as Vt[t][j]
+  __shared__ float coef[RP];
+  __shared__ __attribute__((aligned(16))) bf16 tw[DR_COLS][DR_ROWS + 8]; // tile of W = T^T
   const int b = blockIdx.z;
-  const int i0 = blockIdx.y * DT, j0 = blockIdx.x * DT;
+  const int i0 = blockIdx.y * DR_ROWS, j0 = blockIdx.x * DR_COLS;
   const int tid = threadIdx.x;
   const int k = kvec[b];
+  const float d = dvec[b];
   const float* Ab = A + (long long)b * n * m;
-  for (int e = tid; e < DT * RP; e += 256) {
-    const int rr = e / RP, t = e % RP;
-    const int gi = i0 + rr, gj = j0 + rr;
-    Us[rr][t] = (t < k && gi < n) ? U[((long long)b * n + gi) * RP + t] : 0.f;
-    Vt[t][rr] = (t < k && gj < m) ? V[((long long)b * m + gj) * RP + t] : 0.f;
+  const int k4 = (k + 3) >> 2;                      // float4 chunks of the head columns
+  for (int e = tid; e < DR_ROWS * 16; e += 256) {   // U rows
+    const int rr = e >> 4, t4 = e & 15;
+    const int gi = i0 + rr;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t4 < k4 && gi < n) v = *(const float4*)&U[((long long)b * n + gi) * RP + 4 * t4];
+    Us[rr][4 * t4] = v.x; Us[rr][4 * t4 + 1] = v.y; Us[rr][4 * t4 + 2] = v.z; Us[rr][4 * t4 + 3] = v.w;
   }
-  if (tid < RP) { cws[tid] = cw[b * RP + tid]; crs[tid] = cr[b * RP + tid]; }
+  for (int e = tid; e < DR_COLS * 16; e += 256) {   // V rows, transposed
+    const int cc = e >> 4, t4 = e & 15;
+    const int gj = j0 + cc;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t4 < k4 && gj < m) v = *(const float4*)&V[((long long)b * m + gj) * RP + 4 * t4];
+    Vt[4 * t4][cc] = v.x; Vt[4 * t4 + 1][cc] = v.y; Vt[4 * t4 + 2][cc] = v.z; Vt[4 * t4 + 3][cc] = v.w;
+  }
+  if (tid < RP) coef[tid] = cw[b * RP + tid] / d - cr[b * RP + tid];
   __syncthreads();
-  const int c4 = (tid & 15) * 4;         // 4 consecutive columns
-  const int rb = tid >> 4;               // rows rb, rb + 16, rb + 32, rb + 48
-  float w[4][4], h[4][4];
+  const int c4 = (tid & 31) * 4;      // 4 consecutive columns of the tile
+  const int rw = tid >> 5;            // rows rw + 8a, a = 0..7
+  const bool vec = (m & 3) == 0;
+  float x[8][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int gi = i0 + rb + 16 * a;
+  for (int a = 0; a < 8; ++a) {
+    const int gi = i0 + rw + 8 * a, gj = j0 + c4;
+    if (gi < n && vec && gj + 3 < m) {
+      const float4 v = *(const float4*)&Ab[(long long)gi * m + gj];
+      x[a][0] = v.x / d; x[a][1] = v.y / d; x[a][2] = v.z / d; x[a][3] = v.w / d;
+    } else {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int gj = j0 + c4 + c;
-      w[a][c] = (gi < n && gj < m) ? Ab[(long long)gi * m + gj] : 0.f;
-      h[a][c] = 0.f;
+      for (int c = 0; c < 4; ++c)
+        x[a][c] = (gi < n && gj + c < m) ? Ab[(long long)gi * m + gj + c] / d : 0.f;
     }
   }
   for (int t = 0; t < k; ++t) {
     const float4 v = *(const float4*)&Vt[t][c4];
-    const float vv[4] = {v.x, v.y, v.z, v.w};
+    const float ct = coef[t];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const float u = Us[rb + 16 * a][t];
-      const float uw = u * cws[t];
-      const float ur = u * crs[t];
+    for (int a = 0; a < 8; ++a) {
+      const float u = Us[rw + 8 * a][t] * ct;
+      x[a][0] = fmaf(-u, v.x, x[a][0]);
+      x[a][1] = fmaf(-u, v.y, x[a][1]);
+      x[a][2] = fmaf(-u, v.z, x[a][2]);
+      x[a][3] = fmaf(-u, v.w, x[a][3]);
+    }
+  }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        w[a][c] = fmaf(-uw, vv[c], w[a][c]);
-        if (RESTORE) h[a][c] = fmaf(ur, vv[c], h[a][c]);
+  for (int a = 0; a < 8; ++a) {
+    const int il = rw + 8 * a;
+    const int gi = i0 + il, gj = j0 + c4;
+    bf16x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = f2bf((gi < n && gj + c < m) ? x[a][c] : 0.f);
+    if (x0_mode && gi < n) {
+      const long long off = (long long)b * n * m + (long long)gi * m + gj;
+      if (x0_mode == 1 && vec && gj + 3 < m) {
+        *(bf16x4*)((bf16*)X0 + off) = o;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (gj + c >= m) continue;
+          if (x0_mode == 1) ((bf16*)X0)[off + c] = o[c];
+          else ((float*)X0)[off + c] = x[a][c];
+        }
       }
     }
+    if (T && gi < np && gj < mp)
+      *(bf16x4*)(T + (long long)b * np * mp + (long long)gi * mp + gj) = o;
+    if (W) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) tw[c4 + c][il] = o[c];
+    }
   }
-  if (!RESTORE) {
-    double s = 0.0;
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) s += (double)w[a][c] * (double)w[a][c];
-    red[tid] = s;
+  if (W) {
     __syncthreads();
-    for (int wdt = 128; wdt > 0; wdt >>= 1) {
-      if (tid < wdt) red[tid] += red[tid + wdt];
-      __syncthreads();
-    }
-    if (tid == 0) {
-      const long long tiles = (long long)gridDim.x * gridDim.y;
-      npart[(long long)b * tiles + blockIdx.y * gridDim.x + blockIdx.x] = red[0];
-    }
-  } else {
-    const float d = dvec[b];
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int gi = i0 + rb + 16 * a;
-      if (gi >= n) continue;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int gj = j0 + c4 + c;
-        if (gj >= m) continue;
-        const float x = w[a][c] / d + h[a][c];
-        const long long off = (long long)b * n * m + (long long)gi * m + gj;
-        if (out_bf16) ((bf16*)X0)[off] = f2bf(x);
-        else ((float*)X0)[off] = x;
-      }
+    // row jj of W's tile: DR_ROWS bf16 = 8 chunks of 16 bytes
+    for (int e = tid; e < DR_COLS * 8; e += 256) {
+      const int jj = e >> 3, ch = (e & 7) * 8;
+      const int gj = j0 + jj, gi = i0 + ch;
+      if (gj < mp && gi < np)
+        *(uint4*)(W + (long long)b * mp * np + (long long)gj * np + gi) = *(const uint4*)&tw[jj][ch];
     }
   }
-}
-
-__global__ __launch_bounds__(256) void finish_norm(const double* __restrict__ npart, int tiles,
-                                                   float* __restrict__ d) {
-  __shared__ double red[256];
-  const int b = blockIdx.x, tid = threadIdx.x;
-  double s = 0.0;
-  for (int t = tid; t < tiles; t += 256) s += npart[(long long)b * tiles + t];
-  red[tid] = s;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (tid < w) red[tid] += red[tid + w];
-    __syncthreads();
-  }
-  if (tid == 0) d[b] = (float)sqrt(red[0]) + 1e-7f;
 }
 
 // strided copy of the first r of RP columns: dst (B, rows, r) contiguous
@@ -536,9 +670,9 @@ __global__ __launch_bounds__(256) void copy_cols(const float* __restrict__ src, 
 // ---------------------------------------------------------------------------
 struct RsvdWs {
   float *Y, *Q, *Z, *Zq, *Bt, *U, *V, *M, *Ub, *UbS, *cw, *cr, *s;
-  double *gram, *npart;
+  double *gram, *gramq, *asq;
+  long long* k64;
   int *kint, *degen;
-  float* d;
   size_t bytes;
 };
 
@@ -564,10 +698,10 @@ static RsvdWs rsvd_layout(void* base, int B, int n, int m) {
   w.cw = (float*)take((size_t)B * RP * sizeof(float));
   w.cr = (float*)take((size_t)B * RP * sizeof(float));
   w.s = (float*)take((size_t)B * RP * sizeof(float));
-  w.d = (float*)take((size_t)B * sizeof(float));
   w.gram = (double*)take((size_t)B * GRAM_CHUNKS * RP * RP * sizeof(double));
-  const size_t tiles = (size_t)ceil_div(n, DT) * ceil_div(m, DT);
-  w.npart = (double*)take((size_t)B * tiles * sizeof(double));
+  w.gramq = (double*)take((size_t)B * GRAM_CHUNKS * RP * RP * sizeof(double));
+  w.asq = (double*)take((size_t)B * ceil_div(n, SG_ROWS) * sizeof(double));
+  w.k64 = (long long*)take((size_t)B * sizeof(long long));
   w.kint = (int*)take((size_t)B * sizeof(int));
   w.degen = (int*)take((size_t)B * sizeof(int));
   w.bytes = off;
@@ -583,31 +717,38 @@ static int check_dims(const char* what, int B, int n, int m, int r) {
   return DMH_OK;
 }
 
-// Y = A X (rows n) or Y = A^T X (rows m)
+// Y = A X (rows n) or Y = A^T X (rows m); asq: per-workgroup sums of squares of A
 static int sg(hipStream_t st, int mode, const float* A, int B, int n, int m, const float* X,
-              int ld_x, int xcols, long long x_bs, float* C, long long c_bs) {
+              int ld_x, int xcols, long long x_bs, float* C, long long c_bs,
+              double* asq = nullptr) {
   const int outrows = mode == SG_ROWSTREAM ? n : m;
   dim3 grid(ceil_div(outrows, SG_ROWS), B);
   if (mode == SG_ROWSTREAM)
     hipLaunchKernelGGL(skinny_gemm<SG_ROWSTREAM>, grid, dim3(256), 0, st, A, n, m,
-                       (long long)n * m, X, ld_x, xcols, x_bs, C, c_bs);
+                       (long long)n * m, X, ld_x, xcols, x_bs, C, c_bs, asq);
   else
     hipLaunchKernelGGL(skinny_gemm<SG_COLSTREAM>, grid, dim3(256), 0, st, A, n, m,
-                       (long long)n * m, X, ld_x, xcols, x_bs, C, c_bs);
+                       (long long)n * m, X, ld_x, xcols, x_bs, C, c_bs, (double*)nullptr);
   DMH_CHECK_LAUNCH("skinny_gemm");
   return DMH_OK;
 }
 
-// Q = orth(Y) by CholeskyQR (Y, Q: rows x RP), `passes` times; Q may alias nothing.
+static int gram(hipStream_t st, const float* Y, int B, int rows, double* part) {
+  hipLaunchKernelGGL(gram_partials, dim3(GRAM_CHUNKS, B), dim3(256), 0, st, Y, rows,
+                     (long long)rows * RP, part);
+  DMH_CHECK_LAUNCH("gram_partials");
+  return DMH_OK;
+}
+
+// Q = orth(Y) by CholeskyQR (Y, Q: rows x RP), `passes` times.
 static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int rows, int r,
                 int passes, const RsvdWs& w) {
   const float* src = Y;
+  int rc;
   for (int p = 0; p < passes; ++p) {
     float* dst = (p == passes - 1) ? Q : (p % 2 == 0 ? tmp : Q);
-    hipLaunchKernelGGL(gram_partials, dim3(GRAM_CHUNKS, B), dim3(256), 0, st, src, rows,
-                       (long long)rows * RP, w.gram);
-    DMH_CHECK_LAUNCH("gram_partials");
-    hipLaunchKernelGGL(chol_inv, dim3(B), dim3(256), 0, st, w.gram, r, w.M, w.degen);
+    if ((rc = gram(st, src, B, rows, w.gram))) return rc;
+    hipLaunchKernelGGL(chol_inv, dim3(B), dim3(64), 0, st, w.gram, r, w.M, w.degen);
     DMH_CHECK_LAUNCH("chol_inv");
     hipLaunchKernelGGL(right_mult, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, src, rows,
                        (long long)rows * RP, w.M, dst, (long long)rows * RP);
@@ -622,15 +763,15 @@ static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int
 }
 
 // The subspace iteration and Rayleigh-Ritz: leaves U (n x RP), V (m x RP), the
-// gate outputs and s in the workspace.
+// gate outputs and s in the workspace; with d != nullptr also d = ||W||_F + 1e-7.
 static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, int n, int m,
                      int r, int niter, int passes, const GateParams& gp, long long* k_out,
-                     const RsvdWs& w) {
+                     float* d, const RsvdWs& w) {
   int rc;
   hipMemsetAsync(w.degen, 0, (size_t)B * sizeof(int), st);
-  // Y = A Omega ; Q = orth(Y)
+  // Y = A Omega (and ||A||^2 partials) ; Q = orth(Y)
   if ((rc = sg(st, SG_ROWSTREAM, A, B, n, m, Omega, r, r, (long long)m * r, w.Y,
-               (long long)n * RP)))
+               (long long)n * RP, d ? w.asq : nullptr)))
     return rc;
   if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w))) return rc;
   for (int it = 0; it < niter; ++it) {
@@ -648,11 +789,11 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
   if ((rc = sg(st, SG_COLSTREAM, A, B, n, m, w.Q, RP, RP, (long long)n * RP, w.Bt,
                (long long)m * RP)))
     return rc;
-  hipLaunchKernelGGL(gram_partials, dim3(GRAM_CHUNKS, B), dim3(256), 0, st, w.Bt, m,
-                     (long long)m * RP, w.gram);
-  DMH_CHECK_LAUNCH("gram_partials (Bp)");
-  hipLaunchKernelGGL(eig_gate, dim3(B), dim3(256), 0, st, w.gram, gp, w.degen, w.s, RP, w.Ub,
-                     w.UbS, k_out, w.kint, w.cw, w.cr);
+  if ((rc = gram(st, w.Bt, B, m, w.gram))) return rc;
+  if (d && (rc = gram(st, w.Q, B, n, w.gramq))) return rc;
+  hipLaunchKernelGGL(eig_gate, dim3(B), dim3(64), 0, st, w.gram, gp, w.degen, w.s, RP, w.Ub,
+                     w.UbS, k_out, w.kint, w.cw, w.cr, d ? w.gramq : nullptr,
+                     d ? w.asq : nullptr, ceil_div(n, SG_ROWS), d);
   DMH_CHECK_LAUNCH("eig_gate");
   // U = Q Ub ; V = Bp^T Ub diag(1/s)
   hipLaunchKernelGGL(right_mult, dim3(ceil_div(n, 64), B), dim3(256), 0, st, w.Q, n,
@@ -662,6 +803,24 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
                      (long long)m * RP, w.UbS, w.V, (long long)m * RP);
   DMH_CHECK_LAUNCH("right_mult (V)");
   return DMH_OK;
+}
+
+static int launch_restore(hipStream_t st, const float* A, int B, int n, int m, const RsvdWs& w,
+                          const float* d, void* X0, int x0_mode, bf16* T, bf16* W, int np,
+                          int mp) {
+  const int rows = T ? np : n, cols = T ? mp : m;
+  dim3 grid(ceil_div(cols, DR_COLS), ceil_div(rows, DR_ROWS), B);
+  hipLaunchKernelGGL(deflate_restore, grid, dim3(256), 0, st, A, n, m, w.U, w.V, w.kint, w.cw,
+                     w.cr, d, X0, x0_mode, T, W, np, mp);
+  DMH_CHECK_LAUNCH("deflate_restore");
+  return DMH_OK;
+}
+
+static size_t fused_bytes(int B, int n, int m, size_t* chain_off) {
+  const size_t rs = rsvd_layout(nullptr, B, n, m).bytes;
+  const size_t cb = chain_ws(nullptr, B, chain_dims(n, m, 1)).bytes;
+  if (chain_off) *chain_off = align_up(rs);
+  return align_up(rs) + cb;
 }
 
 }  // namespace dmh
@@ -682,6 +841,16 @@ int dmh_rsvd_workspace_size(int batch, int n, int m, int r, size_t* bytes) {
 
 int dmh_rmfro_workspace_size(int batch, int n, int m, int r, size_t* bytes) {
   return dmh_rsvd_workspace_size(batch, n, m, r, bytes);
+}
+
+int dmh_deflated_polar_workspace_size(int batch, int n, int m, int r, size_t* bytes) {
+  if (!bytes) {
+    set_error("dmh_deflated_polar_workspace_size: null output");
+    return DMH_EINVAL;
+  }
+  if (check_dims("dmh_deflated_polar_workspace_size", batch, n, m, r)) return DMH_EINVAL;
+  *bytes = fused_bytes(batch, n, m, nullptr);
+  return DMH_OK;
 }
 
 int dmh_orth(hipStream_t stream, const float* X, int batch, int rows, int r, int passes,
@@ -705,70 +874,21 @@ int dmh_orth(hipStream_t stream, const float* X, int batch, int rows, int r, int
   DMH_CHECK_LAUNCH("dmh_orth pack");
   int rc = orth(stream, w.Y, w.Q, w.U, batch, rows, r, passes, w);
   if (rc) return rc;
-  hipLaunchKernelGGL(copy_cols, dim3(ceil_div((long long)rows * r, 256) > 4096 ? 4096 : ceil_div((long long)rows * r, 256), batch),
-                     dim3(256), 0, stream, w.Q, rows, r, Q);
+  const int gb = ceil_div((long long)rows * r, 256) > 4096 ? 4096 : ceil_div((long long)rows * r, 256);
+  hipLaunchKernelGGL(copy_cols, dim3(gb, batch), dim3(256), 0, stream, w.Q, rows, r, Q);
   DMH_CHECK_LAUNCH("copy_cols");
   return DMH_OK;
 }
 
-int dmh_rsvd(hipStream_t stream, const float* A, const float* Omega, int batch, int n, int m,
-             int r, int niter, int qr_passes, float* U, float* s, float* V, void* ws,
-             size_t ws_bytes) {
-  if (batch == 0) return DMH_OK;
-  if (!A || !Omega || !U || !s || !V || niter < 0 || qr_passes < 0) {
-    set_error("dmh_rsvd: bad arguments (niter=%d qr_passes=%d)", niter, qr_passes);
-    return DMH_EINVAL;
-  }
-  if (check_dims("dmh_rsvd", batch, n, m, r)) return DMH_EINVAL;
-  RsvdWs w = rsvd_layout(ws, batch, n, m);
-  if (!ws || ws_bytes < w.bytes) {
-    set_error("dmh_rsvd: workspace %zu < %zu bytes", ws_bytes, w.bytes);
-    return DMH_EWORKSPACE;
-  }
-  GateParams gp{r, 1, 0.f, 0.f, 1.f};
-  long long* kdummy = (long long*)w.npart;   // gate outputs unused here
-  int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, kdummy, w);
-  if (rc) return rc;
+static int copy_usv(hipStream_t stream, const RsvdWs& w, int batch, int n, int m, int r,
+                    float* U, float* s, float* V) {
   const int gb = ceil_div((long long)n * r, 256) > 4096 ? 4096 : ceil_div((long long)n * r, 256);
   hipLaunchKernelGGL(copy_cols, dim3(gb, batch), dim3(256), 0, stream, w.U, n, r, U);
   const int gm = ceil_div((long long)m * r, 256) > 4096 ? 4096 : ceil_div((long long)m * r, 256);
   hipLaunchKernelGGL(copy_cols, dim3(gm, batch), dim3(256), 0, stream, w.V, m, r, V);
   hipMemcpy2DAsync(s, r * sizeof(float), w.s, RP * sizeof(float), r * sizeof(float), batch,
                    hipMemcpyDeviceToDevice, stream);
-  DMH_CHECK_LAUNCH("dmh_rsvd outputs");
-  return DMH_OK;
-}
-
-int dmh_rmfro_clip(hipStream_t stream, const float* A, const float* Omega, int batch, int n,
-                   int m, int r, int kw, float ratio, float thresh, float pad, int niter,
-                   int qr_passes, void* X0, int out_bf16, long long* k, float* d, void* ws,
-                   size_t ws_bytes) {
-  if (batch == 0) return DMH_OK;
-  if (!A || !Omega || !X0 || !k || !d || kw < 1 || kw > r || niter < 0 || qr_passes < 0 ||
-      !(pad > 0.f)) {
-    set_error("dmh_rmfro_clip: bad arguments (kw=%d r=%d niter=%d qr_passes=%d pad=%g)", kw, r,
-              niter, qr_passes, (double)pad);
-    return DMH_EINVAL;
-  }
-  if (check_dims("dmh_rmfro_clip", batch, n, m, r)) return DMH_EINVAL;
-  RsvdWs w = rsvd_layout(ws, batch, n, m);
-  if (!ws || ws_bytes < w.bytes) {
-    set_error("dmh_rmfro_clip: workspace %zu < %zu bytes", ws_bytes, w.bytes);
-    return DMH_EWORKSPACE;
-  }
-  GateParams gp{r, kw, ratio, thresh, pad};
-  int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, k, w);
-  if (rc) return rc;
-  dim3 grid(ceil_div(m, DT), ceil_div(n, DT), batch);
-  const int tiles = grid.x * grid.y;
-  hipLaunchKernelGGL(deflate_tile<false>, grid, dim3(256), 0, stream, A, n, m, w.U, w.V, w.kint,
-                     w.cw, w.cr, w.npart, nullptr, nullptr, 0);
-  DMH_CHECK_LAUNCH("deflate_tile (norm)");
-  hipLaunchKernelGGL(finish_norm, dim3(batch), dim3(256), 0, stream, w.npart, tiles, d);
-  DMH_CHECK_LAUNCH("finish_norm");
-  hipLaunchKernelGGL(deflate_tile<true>, grid, dim3(256), 0, stream, A, n, m, w.U, w.V, w.kint,
-                     w.cw, w.cr, nullptr, d, X0, out_bf16);
-  DMH_CHECK_LAUNCH("deflate_tile (restore)");
+  DMH_CHECK_LAUNCH("U, s, V outputs");
   return DMH_OK;
 }
 
@@ -793,26 +913,103 @@ int dmh_project(hipStream_t stream, const float* Q, const float* A, int batch, i
   int rc = sg(stream, SG_COLSTREAM, A, batch, n, m, w.Q, RP, RP, (long long)n * RP, w.Bt,
               (long long)m * RP);
   if (rc) return rc;
-  hipLaunchKernelGGL(gram_partials, dim3(GRAM_CHUNKS, batch), dim3(256), 0, stream, w.Bt, m,
-                     (long long)m * RP, w.gram);
-  DMH_CHECK_LAUNCH("gram_partials (Bp)");
+  if ((rc = gram(stream, w.Bt, batch, m, w.gram))) return rc;
   GateParams gp{r, 1, 0.f, 0.f, 1.f};
-  hipLaunchKernelGGL(eig_gate, dim3(batch), dim3(256), 0, stream, w.gram, gp, w.degen, w.s, RP,
-                     w.Ub, w.UbS, (long long*)w.npart, w.kint, w.cw, w.cr);
+  hipLaunchKernelGGL(eig_gate, dim3(batch), dim3(64), 0, stream, w.gram, gp, w.degen, w.s, RP,
+                     w.Ub, w.UbS, w.k64, w.kint, w.cw, w.cr, (const double*)nullptr,
+                     (const double*)nullptr, 0, (float*)nullptr);
   DMH_CHECK_LAUNCH("eig_gate");
   hipLaunchKernelGGL(right_mult, dim3(ceil_div(n, 64), batch), dim3(256), 0, stream, w.Q, n,
                      (long long)n * RP, w.Ub, w.U, (long long)n * RP);
   hipLaunchKernelGGL(right_mult, dim3(ceil_div(m, 64), batch), dim3(256), 0, stream, w.Bt, m,
                      (long long)m * RP, w.UbS, w.V, (long long)m * RP);
   DMH_CHECK_LAUNCH("right_mult (U, V)");
-  const int gb = ceil_div((long long)n * r, 256) > 4096 ? 4096 : ceil_div((long long)n * r, 256);
-  hipLaunchKernelGGL(copy_cols, dim3(gb, batch), dim3(256), 0, stream, w.U, n, r, U);
-  const int gm = ceil_div((long long)m * r, 256) > 4096 ? 4096 : ceil_div((long long)m * r, 256);
-  hipLaunchKernelGGL(copy_cols, dim3(gm, batch), dim3(256), 0, stream, w.V, m, r, V);
-  hipMemcpy2DAsync(s, r * sizeof(float), w.s, RP * sizeof(float), r * sizeof(float), batch,
-                   hipMemcpyDeviceToDevice, stream);
-  DMH_CHECK_LAUNCH("dmh_project outputs");
-  return DMH_OK;
+  return copy_usv(stream, w, batch, n, m, r, U, s, V);
+}
+
+int dmh_rsvd(hipStream_t stream, const float* A, const float* Omega, int batch, int n, int m,
+             int r, int niter, int qr_passes, float* U, float* s, float* V, void* ws,
+             size_t ws_bytes) {
+  if (batch == 0) return DMH_OK;
+  if (!A || !Omega || !U || !s || !V || niter < 0 || qr_passes < 0) {
+    set_error("dmh_rsvd: bad arguments (niter=%d qr_passes=%d)", niter, qr_passes);
+    return DMH_EINVAL;
+  }
+  if (check_dims("dmh_rsvd", batch, n, m, r)) return DMH_EINVAL;
+  RsvdWs w = rsvd_layout(ws, batch, n, m);
+  if (!ws || ws_bytes < w.bytes) {
+    set_error("dmh_rsvd: workspace %zu < %zu bytes", ws_bytes, w.bytes);
+    return DMH_EWORKSPACE;
+  }
+  GateParams gp{r, 1, 0.f, 0.f, 1.f};
+  int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, w.k64, nullptr, w);
+  if (rc) return rc;
+  return copy_usv(stream, w, batch, n, m, r, U, s, V);
+}
+
+static int clip_args(const char* what, const float* A, const float* Omega, const void* X0,
+                     const long long* k, const float* d, int batch, int n, int m, int r, int kw,
+                     int niter, int qr_passes, float pad) {
+  if (!A || !Omega || !X0 || !k || !d || kw < 1 || kw > r || niter < 0 || qr_passes < 0 ||
+      !(pad > 0.f)) {
+    set_error("%s: bad arguments (kw=%d r=%d niter=%d qr_passes=%d pad=%g)", what, kw, r, niter,
+              qr_passes, (double)pad);
+    return DMH_EINVAL;
+  }
+  return check_dims(what, batch, n, m, r);
+}
+
+int dmh_rmfro_clip(hipStream_t stream, const float* A, const float* Omega, int batch, int n,
+                   int m, int r, int kw, float ratio, float thresh, float pad, int niter,
+                   int qr_passes, void* X0, int out_bf16, long long* k, float* d, void* ws,
+                   size_t ws_bytes) {
+  if (batch == 0) return DMH_OK;
+  if (clip_args("dmh_rmfro_clip", A, Omega, X0, k, d, batch, n, m, r, kw, niter, qr_passes, pad))
+    return DMH_EINVAL;
+  RsvdWs w = rsvd_layout(ws, batch, n, m);
+  if (!ws || ws_bytes < w.bytes) {
+    set_error("dmh_rmfro_clip: workspace %zu < %zu bytes", ws_bytes, w.bytes);
+    return DMH_EWORKSPACE;
+  }
+  GateParams gp{r, kw, ratio, thresh, pad};
+  int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, k, d, w);
+  if (rc) return rc;
+  return launch_restore(stream, A, batch, n, m, w, d, X0, out_bf16 ? 1 : 2, nullptr, nullptr, 0,
+                        0);
+}
+
+int dmh_deflated_polar(hipStream_t stream, const float* A, const float* Omega, int batch, int n,
+                       int m, int r, int kw, float ratio, float thresh, float pad, int niter,
+                       int qr_passes, const double* coeffs, int steps, void* out, long long* k,
+                       float* d, void* ws, size_t ws_bytes, void* chain_event) {
+  if (batch == 0) return DMH_OK;
+  if (clip_args("dmh_deflated_polar", A, Omega, out, k, d, batch, n, m, r, kw, niter, qr_passes,
+                pad))
+    return DMH_EINVAL;
+  if (steps < 0 || (steps > 0 && !coeffs)) {
+    set_error("dmh_deflated_polar: bad steps/coeffs (steps=%d)", steps);
+    return DMH_EINVAL;
+  }
+  size_t chain_off = 0;
+  const size_t need = fused_bytes(batch, n, m, &chain_off);
+  if (!ws || ws_bytes < need) {
+    set_error("dmh_deflated_polar: workspace %zu < %zu bytes", ws_bytes, need);
+    return DMH_EWORKSPACE;
+  }
+  RsvdWs w = rsvd_layout(ws, batch, n, m);
+  const ChainDims cd = chain_dims(n, m, 1);
+  const ChainWs cw = chain_ws((char*)ws + chain_off, batch, cd);
+  GateParams gp{r, kw, ratio, thresh, pad};
+  int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, k, d, w);
+  if (rc) return rc;
+  // X0 goes straight into the chain's packed operands (T and W = T^T)
+  if ((rc = launch_restore(stream, A, batch, n, m, w, d, nullptr, 0, cw.T0, cw.W0, cd.np, cd.mp)))
+    return rc;
+  if (chain_event && hipEventRecord((hipEvent_t)chain_event, stream) != hipSuccess) {
+    set_error("dmh_deflated_polar: hipEventRecord failed");
+    return DMH_ELAUNCH;
+  }
+  return chain_run_packed(stream, cw, batch, cd, 1, coeffs, steps, (bf16*)out);
 }
 
 }  // extern "C"

@@ -37,6 +37,12 @@ _SIGS = {
     "dmh_rmfro_clip": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_float,
                                c_float, c_float, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp,
                                c_sz]),
+    "dmh_deflated_polar_workspace_size": (c_int, [c_int, c_int, c_int, c_int,
+                                                  ctypes.POINTER(c_sz)]),
+    "dmh_deflated_polar": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_float,
+                                   c_float, c_float, c_int, c_int,
+                                   ctypes.POINTER(ctypes.c_double), c_int, c_vp, c_vp, c_vp,
+                                   c_vp, c_sz, c_vp]),
 }
 
 # largest sketch width the front-end kernels carry (include/defmuon_hip.h)
@@ -204,3 +210,33 @@ def rmfro_clip(A, Omega, kw, ratio, thresh, pad, niter=1, passes=1, out_dtype=No
     if out_dtype is not None and not bf and out_dtype != torch.float32:
         X0 = X0.to(out_dtype)
     return X0, k, d
+
+
+def deflated_polar(A, Omega, kw, ratio, thresh, pad, coeffs, niter=1, passes=1,
+                   chain_event=None):
+    """Front-end + bf16 chain in one call on a tall group A (B, n, m): returns the
+    polar factors (B, n, m) bf16, k (B,) int64 and d (B,) fp32.  chain_event: a
+    torch.cuda.Event (already recorded once, so that its HIP event exists) that the
+    library re-records between the front-end and the chain."""
+    A, Omega = _f32c(A, "deflated_polar"), _f32c(Omega, "deflated_polar")
+    B, n, m = A.shape
+    r = Omega.shape[-1]
+    out = torch.empty((B, n, m), dtype=torch.bfloat16, device=A.device)
+    k = torch.empty((B,), dtype=torch.int64, device=A.device)
+    d = torch.empty((B,), dtype=torch.float32, device=A.device)
+    if B == 0:
+        return out, k, d
+    lib = load()
+    nbytes = c_sz()
+    _check(lib.dmh_deflated_polar_workspace_size(B, n, m, r, ctypes.byref(nbytes)),
+           "dmh_deflated_polar_workspace_size")
+    ws = _workspace(nbytes.value, A.device)
+    steps = len(coeffs)
+    flat = (ctypes.c_double * max(3 * steps, 1))(*[float(v) for t in coeffs for v in t])
+    _check(lib.dmh_deflated_polar(_stream(A.device), _ptr(A), _ptr(Omega), B, n, m, r, int(kw),
+                                  float(ratio), float(thresh), float(pad), int(niter),
+                                  int(passes), flat, steps, _ptr(out), _ptr(k), _ptr(d),
+                                  _ptr(ws), nbytes.value,
+                                  c_vp(chain_event.cuda_event if chain_event is not None else 0)),
+           "dmh_deflated_polar")
+    return out, k, d

@@ -151,17 +151,47 @@ def _horner_iterate(X, hs):
 
 class _DeflatedPolarBase:
     """A deflated arm: the batched fp32 setup, then a subclass-chosen bf16
-    iteration.  Subclasses supply `_iterate`."""
+    iteration.  Subclasses supply `_iterate` (and, for the fused path,
+    `schedule`)."""
     PAD = DIVISOR_PAD
     BATCHED_CLIP = staticmethod(batched_rmfro_clip)
 
     def _iterate(self, X, steps):
         raise NotImplementedError
 
+    def schedule(self, steps):
+        """The (a, b, c) triples `_iterate` applies, or None if unknown."""
+        return None
+
+    def polar_group(self, A, generator=None, steps=5, Omega=None, chain_event=None):
+        """BATCHED_CLIP(A, bf16) then `_iterate` for one tall shape group, as
+        muon.py:298,310-312 run them.  For the built-in arms both run in one
+        library call (dmh_deflated_polar) that hands X0 to the chain in its packed
+        layout; an arm that overrides BATCHED_CLIP or `_iterate` gets exactly its
+        own two calls.  Returns (polar factors (B, n, m) bf16, k, d).  chain_event
+        (fused path only): a torch.cuda.Event recorded between the two phases."""
+        cls = type(self)
+        hs = self.schedule(steps)
+        fused = (hs is not None and cls.BATCHED_CLIP is _DeflatedPolarBase.BATCHED_CLIP
+                 and cls._iterate in (DeflatedNSPolar._iterate, DeflatedPEPolar._iterate))
+        if not fused:
+            X0, k, d = self.BATCHED_CLIP(A, generator=generator, Omega=Omega, pad=self.PAD,
+                                         out_dtype=torch.bfloat16)
+            return self._iterate(X0, steps), k, d
+        Bn, n, m = A.shape
+        r, kw = sketch_dims(m)
+        if Omega is None:
+            Omega = torch.randn(Bn, m, r, device=A.device, dtype=A.dtype, generator=generator)
+        return _native.deflated_polar(A, Omega, kw, GATE_RATIO, DEFLATE_THRESH, self.PAD, hs,
+                                      RSVD_NITER, CHOLQR_PASSES, chain_event)
+
 
 class DeflatedNSPolar(_DeflatedPolarBase):
     """The standard Newton-Schulz quintic behind the deflation."""
     NS_ABC = (3.4445, -4.7750, 2.0315)
+
+    def schedule(self, steps):
+        return [self.NS_ABC] * steps
 
     def _iterate(self, X, steps):
         return _horner_iterate(X, [self.NS_ABC] * steps)
@@ -171,6 +201,10 @@ class DeflatedPEPolar(_DeflatedPolarBase):
     """The Polar Express schedule behind the deflation; PAD defaults to 1.1
     (DEFMUON_DEFL_PE_PAD)."""
     PAD = float(os.environ.get("DEFMUON_DEFL_PE_PAD", "1.1"))
+
+    def schedule(self, steps):
+        from defmuon_amd.optim.polar_express import pe_schedule
+        return pe_schedule(steps)
 
     def _iterate(self, X, steps):
         from defmuon_amd.optim.polar_express import pe_schedule

@@ -5,11 +5,12 @@ contract (muon.py:16-44) and the same `Muon` optimizer API, parameter routing,
 W_QKV split, batched deflated step, sketch seeding, gate statistics, learning
 rate scaling and AdamW backup (muon.py:47-438).
 
-One execution difference, with identical per-matrix results: the deflated step
-runs the bf16 iteration once per tall-shape group (one grouped launch per GEMM
-phase over every matrix of the group) instead of once per parameter
-(muon.py:309-312).  Each matrix's iteration is independent of the others in the
-batch, so the outputs are the same matrices the per-parameter calls produce.
+Execution differences, with identical per-matrix results: the deflated step runs
+the bf16 iteration once per tall-shape group (one grouped launch per GEMM phase
+over every matrix of the group) instead of once per parameter (muon.py:309-312),
+and for the built-in arms the clip and the iteration are one library call that
+hands X0 to the chain in its packed layout (`_DeflatedPolarBase.polar_group`).
+Each matrix's computation is independent of the others in the batch.
 """
 
 import math
@@ -184,18 +185,20 @@ class Muon(torch.optim.Optimizer):
             gen.manual_seed((self._bd_step * 1009 + gi * 9176867) % (2 ** 62))
             timed = _TIMING_ON[0] and A.is_cuda
             if timed:
+                # separate clip and iteration calls so the events can split them
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
                 e0.record()
-            X0, kvec, _ = fac.BATCHED_CLIP(A, generator=gen, pad=fac.PAD,
-                                           out_dtype=torch.bfloat16)
-            if timed:
+                X0, kvec, _ = fac.BATCHED_CLIP(A, generator=gen, pad=fac.PAD,
+                                               out_dtype=torch.bfloat16)
                 e1.record()
+                Ug = fac._iterate(X0, ns_steps)      # one grouped launch per GEMM phase
+            else:
+                Ug, kvec, _ = fac.polar_group(A, generator=gen, steps=ns_steps)
             if _GATE_ACC[0] is None or _GATE_ACC[0].device != kvec.device:
                 _GATE_ACC[0] = torch.zeros(3, dtype=torch.int64, device=kvec.device)
             _GATE_ACC[0] += torch.stack([
                 torch.tensor(A.shape[0], dtype=torch.int64, device=kvec.device),
                 (kvec > 0).sum(), kvec.sum().to(torch.int64)])
-            Ug = fac._iterate(X0, ns_steps)          # one grouped launch per GEMM phase
             off = 0
             for e in es:
                 e["u"] = Ug[off:off + e["nb"]]

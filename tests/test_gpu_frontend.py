@@ -160,3 +160,30 @@ def test_zero_matrix_is_declined_and_finite(N):
     assert int(k[1]) == 2
     _, ko, _ = O.rmfro_clip(A[1:], Om[1:])
     assert int(ko[0]) == 2
+
+
+@pytest.mark.parametrize("arm", ["ns", "pe"])
+def test_fused_deflated_polar_matches_two_calls(N, arm):
+    """dmh_deflated_polar (clip written straight into the chain's operands) gives
+    bit-identical results to BATCHED_CLIP followed by _iterate, and both agree
+    with the oracle."""
+    from defmuon_amd.optim import deflation_batched as DB
+    fac = DB.DeflatedNSPolar() if arm == "ns" else DB.DeflatedPEPolar()
+    spec = [((900, 300), dict(seed=60 + i, n_spikes=4, hi=60.0, lo=20.0)) for i in range(3)]
+    spec.append(((900, 300), dict(seed=63, n_spikes=0)))
+    A = _spiked_batch(spec)
+    r, kw = O.sketch_dims(300)
+    Om = O.draw_omega(4, 300, r, 5)
+    Ad, Omd = A.to(DEV), Om.to(DEV)
+    U1, k1, d1 = fac.polar_group(Ad, Omega=Omd, steps=5)
+    X0, k2, d2 = fac.BATCHED_CLIP(Ad, Omega=Omd, pad=fac.PAD, out_dtype=torch.bfloat16)
+    U2 = fac._iterate(X0, 5)
+    assert torch.equal(k1, k2) and torch.equal(d1, d2)
+    assert torch.equal(U1.view(torch.int16), U2.view(torch.int16))
+    assert k1.cpu().tolist() == [4, 4, 4, 0]
+    Xo, ko, do = O.rmfro_clip(A, Om, pad=fac.PAD, out_dtype=torch.bfloat16)
+    hs = O.ns_schedule(5) if arm == "ns" else O.pe_schedule(5)
+    Uo = O.horner_iterate(Xo, hs)
+    from parity import assert_polar_parity
+    for b in range(4):
+        assert_polar_parity(U1[b], Uo[b], A[b], f"fused {arm}[{b}]")
