@@ -11,20 +11,22 @@
 // row-major with m, n rounded up to the 256 tile.  One iteration (a, b, c) is
 //
 //   K1  A  = W W^T                  (m x m, K = n)  symmetric: upper tiles only
-//   K2  B  = b A + c A A            (m x m, K = m)  symmetric: upper tiles only
-//   K3  T' = a T + T B ; W' = T'^T  (n x m, K = m)
+//   K2  B' = b A + c A A + a I      (m x m, K = m)  symmetric: upper tiles only
+//   K3  T' = T B' ; W' = T'^T       (n x m, K = m)
 //
 // so every product is an "NT" GEMM C[i][j] = sum_k P[i][k] Q[j][k] whose two
 // operands are both K-contiguous, which is the layout the MFMA operand
-// registers want (A and B symmetric make A A and T B NT products).  Zero
-// padding is a fixed point of every phase, so no kernel needs bounds checks on
-// its loads.
+// registers want (A and B' symmetric make A A and T B' NT products).  Zero
+// padding is a fixed point of every phase (a I is added on the m true diagonal
+// entries only), so no kernel needs bounds checks on its loads.
 //
-// Rounding follows the reference's compiled graph for batched operands: A is
-// stored bf16; B = bf16(b*A + bf16(c*AA)); T' = bf16(a*T + bf16(TB)).  (The
-// reference rounds c*A to bf16 before the product; this kernel scales the fp32
-// accumulator instead, which keeps A*A symmetric and lets K2 skip half its
-// tiles.)
+// Rounding.  A is stored bf16; B' = bf16(b*A + bf16(c*AA) + a*I); T' = bf16(T B')
+// with fp32 accumulation.  The reference's compiled graph rounds c*A to bf16
+// before the product and forms bf16(a*T + bf16(T B)); this kernel scales the fp32
+// accumulator by c instead (keeps A*A symmetric, so K2 skips half its tiles) and
+// folds a*T into the product through the diagonal of B' (a T + T B = T (B + a I)),
+// which removes K3's read of T and the rounding of T B, a term several times
+// larger than T' itself.
 #include "common.h"
 #include "ns_chain.h"
 
@@ -63,7 +65,7 @@ constexpr int STAGEB = 2 * OPB;              // P + Q
 constexpr int GEMM_THREADS = 256;
 static_assert(NSTAGE * STAGEB == 128 * 1024, "LDS ring must equal the epilogue tile");
 
-enum { EPI_STORE = 0, EPI_POLY = 1, EPI_AXPY = 2 };
+enum { EPI_STORE = 0, EPI_POLY = 1 };
 
 struct GemmArgs {
   const bf16* P; long long p_bs; int p_ld;      // rows i of C
@@ -71,8 +73,9 @@ struct GemmArgs {
   int K;                                         // multiple of TK
   int tiles_m, tiles_n;                          // tiles per matrix
   int sym;                                       // upper-triangular tiles, mirrored stores
-  float alpha, beta;                             // POLY: (b, c); AXPY: (a, -)
-  const bf16* aux; long long aux_bs; int aux_ld; // POLY: A; AXPY: T  (indexed [i][j])
+  float alpha, beta;                             // POLY: (b, c)
+  float diag_add; int diag_lim;                  // POLY: + diag_add on C[i][i], i < diag_lim
+  const bf16* aux; long long aux_bs; int aux_ld; // POLY: A (indexed [i][j])
   bf16* out; long long out_bs; int out_ld;       // C[i][j]   (may be null)
   bf16* outT; long long outT_bs; int outT_ld;    // C[j][i]   (may be null)
   int valid_i, valid_j;                          // stores limited to i < valid_i, j < valid_j
@@ -171,72 +174,101 @@ void gemm_nt_bf16(GemmArgs g) {
   const int fQ = OPB + (128 * wn + r32) * ROWB;
   const int fch0 = ((0 + hi) ^ sw) * 16, fch1 = ((2 + hi) ^ sw) * 16;
 
+  // Main loop, software-pipelined at two levels:
+  //  * LDS ring: stages kt+1..kt+3 are in flight while stage kt is consumed.  The
+  //    prefetch is unconditional: past the last stage it re-fetches the last stage
+  //    into the free slot (never read), so every step waits on the same vmcnt and
+  //    the loop body is one basic block the scheduler can interleave.
+  //  * fragments: the k16 substep-0 fragments of stage kt+1 are read from LDS
+  //    under the substep-1 MFMAs of stage kt, and substep 1 under substep 0, so the
+  //    MFMA pipe never waits on LDS at the top of a step.
+  // Slot (kt+3)&3 refilled at step kt held stage kt-1, whose last fragment reads
+  // completed (lgkmcnt(0)) before the barrier of step kt-1.
   const int nk = g.K / TK;
-  // prologue: stages 0 .. NSTAGE-2 in flight; wait for stage 0
 #pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p)
-    if (p < nk) DMH_GLOAD(p * TK, p);
-  if (nk >= 3) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if (nk == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  ring_barrier();
+  for (int p = 0; p < NSTAGE - 1; ++p) DMH_GLOAD(min(p, nk - 1) * TK, p);
+  asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // stage 0 landed (own loads)
+  ring_barrier();                                       // ... and everyone's
 
+  bf16x8 f0p[4], f0q[4], f1p[4], f1q[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f0p[i] = *(const bf16x8*)(smem + fP + i * 32 * ROWB + fch0);
+    f0q[i] = *(const bf16x8*)(smem + fQ + i * 32 * ROWB + fch0);
+  }
   for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & (NSTAGE - 1);
-    const int pre = kt + NSTAGE - 1;
-    if (pre < nk) DMH_GLOAD(pre * TK, pre & (NSTAGE - 1));
-    const char* base = smem + st * STAGEB;
-    bf16x8 pf[2][4], qf[2][4];
+    const char* cur = smem + (kt & (NSTAGE - 1)) * STAGEB;
+    const char* nxt = smem + ((kt + 1) & (NSTAGE - 1)) * STAGEB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pf[0][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fch0);
-      qf[0][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fch0);
+      f1p[i] = *(const bf16x8*)(cur + fP + i * 32 * ROWB + fch1);
+      f1q[i] = *(const bf16x8*)(cur + fQ + i * 32 * ROWB + fch1);
     }
+    DMH_GLOAD(min(kt + NSTAGE - 1, nk - 1) * TK, (kt + NSTAGE - 1) & (NSTAGE - 1));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pf[1][i] = *(const bf16x8*)(base + fP + i * 32 * ROWB + fch1);
-      qf[1][i] = *(const bf16x8*)(base + fQ + i * 32 * ROWB + fch1);
-    }
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0q[j], f0p[i], acc[i][j], 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[s][j], pf[s][i], acc[i][j],
-                                                              0, 0, 0);
-    // Schedule: the prefetch loads, the step-0 fragments, then step-1 fragment
-    // reads issued early among the step-0 MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);    // VMEM (direct-to-LDS loads)
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS read: step-0 fragments
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
+    for (int x = 0; x < 8; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (substep-1 fragments)
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 28, 0);
-    // stage kt+1 must be complete; the loads issued after it are those of the
-    // younger stages kt+2 and kt+3 that exist (8 per stage per wave), and loads
-    // retire in issue order
-    if (kt + 3 < nk) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (kt + 2 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (direct-to-LDS prefetch)
+    }
+    // stage kt+1 landed: the younger loads in flight are stages kt+2, kt+3 (8 per
+    // stage per wave), and loads retire in issue order
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
     ring_barrier();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f0p[i] = *(const bf16x8*)(nxt + fP + i * 32 * ROWB + fch0);
+      f0q[i] = *(const bf16x8*)(nxt + fQ + i * 32 * ROWB + fch0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1q[j], f1p[i], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (next substep-0 fragments)
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   }
 #undef DMH_GLOAD
+  // the re-fetches past the last stage may still be landing in LDS
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue -------------------------------------------------------------
   // The 256x256 output tile is staged through LDS as bf16 (the whole 128 KB),
   // so both output layouts leave in 16-byte coalesced stores.
   //   phase 1  acc -> LDS: v = bf16(acc) (bf16(c * acc) for POLY)
-  //   phase 2  row-major pass: epilogue (aux read in 16 B), store C[i][j]
+  //   phase 2  row-major pass: POLY epilogue (aux read in 16 B), store C[i][j]
   //   phase 3  transposed pass: 8 rows x 4 columns per step, transposed in
   //            registers, store C^T[j][i]
   // LDS element (i, j) of the tile sits at byte i*512 + 16*((j>>3) ^ swz(i)) + 2*(j&7);
   // swz(i) = ((i>>3)&3) | ((((i&7) ^ (i>>5)) & 7) << 2) keeps 32 consecutive rows (phase
   // 1) and rows 8 apart (phase 3) on distinct 16-byte slots.
   // acc[i][j][4g+q] holds C[i0 + (lane&31)][j0 + 8g + 4(lane>>5) + q].
-  __syncthreads();
+  // The barriers below only order LDS (lgkmcnt), so the aux tile, fetched in one
+  // batch up front, stays in flight while the accumulators drain.
+  const int gi0 = ti * TILE, gj0 = tj * TILE;
+  bf16x8 av[32];
+  if (EPI == EPI_POLY) {
+    const bf16* auxb = g.aux + (long long)b * g.aux_bs + (long long)gi0 * g.aux_ld + gj0;
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const int e = tid + GEMM_THREADS * u;
+      av[u] = *(const bf16x8*)(auxb + (long long)(e >> 5) * g.aux_ld + (e & 31) * 8);
+    }
+  }
+  ring_barrier();
   char* const cs = smem;
   auto cswz = [](int i) { return ((i >> 3) & 3) | ((((i & 7) ^ (i >> 5)) & 7) << 2); };
   auto caddr = [&](int i, int j) { return i * 512 + 16 * ((j >> 3) ^ cswz(i)) + 2 * (j & 7); };
@@ -258,30 +290,51 @@ void gemm_nt_bf16(GemmArgs g) {
       }
     }
   }
-  __syncthreads();
+  ring_barrier();
   const bool diag = g.sym && ti == tj;
   if (diag) {
-    // exact symmetry: the lower triangle of a diagonal tile takes the upper one's values
-    for (int e = tid; e < TILE * TILE; e += GEMM_THREADS) {
-      const int i = e >> 8, j = e & 255;
-      if (i > j) *(bf16*)(cs + caddr(i, j)) = *(const bf16*)(cs + caddr(j, i));
+    // exact symmetry: the lower triangle of a diagonal tile takes the upper one's
+    // values.  8x8 blocks (I, J), I >= J: block (J, I) is read as 8 rows of 16 B,
+    // transposed in registers and written over block (I, J); on the diagonal
+    // blocks only the strictly lower elements are replaced.  Reads and writes of
+    // one thread touch blocks no other thread writes.
+    for (int blk = tid; blk < 32 * 33 / 2; blk += GEMM_THREADS) {
+      int I = (int)((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
+      while ((I + 1) * (I + 2) / 2 <= blk) ++I;
+      while (I * (I + 1) / 2 > blk) --I;
+      const int J = blk - I * (I + 1) / 2;
+      bf16x8 src[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) src[r] = *(const bf16x8*)(cs + caddr(8 * J + r, 8 * I));
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        bf16x8 d;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) d[r] = src[r][c];
+        if (I == J) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r)
+            if (r >= c) d[r] = src[c][r];
+        }
+        *(bf16x8*)(cs + caddr(8 * I + c, 8 * J)) = d;
+      }
     }
-    __syncthreads();
+    ring_barrier();
   }
-  const int gi0 = ti * TILE, gj0 = tj * TILE;
   const bool need_t = g.outT && (!g.sym || !diag);
-  const bf16* auxb = EPI == EPI_STORE ? nullptr : g.aux + (long long)b * g.aux_bs;
   bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
+#pragma unroll
   for (int u = 0; u < 32; ++u) {
     const int e = tid + GEMM_THREADS * u;
     const int il = e >> 5, jc = (e & 31) * 8;
     char* lp = cs + il * 512 + 16 * ((jc >> 3) ^ cswz(il));
     bf16x8 v = *(const bf16x8*)lp;
     const int gi = gi0 + il, gj = gj0 + jc;
-    if (EPI != EPI_STORE) {
-      const bf16x8 av = *(const bf16x8*)(auxb + (long long)gi * g.aux_ld + gj);
+    if (EPI == EPI_POLY) {
+      const int qd = diag && gi < g.diag_lim ? il - jc : -1;   // the diagonal's slot, if here
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = f2bf(g.alpha * bf2f(av[q]) + bf2f(v[q]));
+      for (int q = 0; q < 8; ++q)
+        v[q] = f2bf(g.alpha * bf2f(av[u][q]) + bf2f(v[q]) + (q == qd ? g.diag_add : 0.f));
       if (need_t) *(bf16x8*)lp = v;
     }
     if (outb && gi < g.valid_i) {
@@ -296,7 +349,7 @@ void gemm_nt_bf16(GemmArgs g) {
     }
   }
   if (!need_t) return;
-  __syncthreads();
+  ring_barrier();
   bf16* outtb = g.outT + (long long)b * g.outT_bs;
   for (int u = 0; u < 8; ++u) {
     const int e = tid + GEMM_THREADS * u;
@@ -506,17 +559,15 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     g2.P = Am; g2.p_bs = (long long)d.mp * d.mp; g2.p_ld = d.mp;
     g2.Q = Am; g2.q_bs = g2.p_bs; g2.q_ld = d.mp;
     g2.K = d.mp;
-    g2.alpha = bcoef; g2.beta = c;
+    g2.alpha = bcoef; g2.beta = c; g2.diag_add = a; g2.diag_lim = d.m;
     g2.aux = Am; g2.aux_bs = g2.p_bs; g2.aux_ld = d.mp;
     g2.out = Bm; g2.outT = Bm;
-    if ((rc = launch_gemm<EPI_POLY>(g2, batch, stream, "ns K2 (bA + cA^2)"))) return rc;
-    // K3: T' = a T + T B  (and W' = T'^T)
+    if ((rc = launch_gemm<EPI_POLY>(g2, batch, stream, "ns K2 (bA + cA^2 + aI)"))) return rc;
+    // K3: T' = T B'  (and W' = T'^T)
     GemmArgs g3{};
     g3.P = Tc; g3.p_bs = (long long)d.np * d.mp; g3.p_ld = d.mp;
     g3.Q = Bm; g3.q_bs = (long long)d.mp * d.mp; g3.q_ld = d.mp;
     g3.K = d.mp; g3.tiles_m = tn; g3.tiles_n = tm; g3.sym = 0;
-    g3.alpha = a;
-    g3.aux = Tc; g3.aux_bs = g3.p_bs; g3.aux_ld = d.mp;
     if (!last) {
       g3.out = Tn; g3.out_bs = g3.p_bs; g3.out_ld = d.mp;
       g3.outT = Wn; g3.outT_bs = (long long)d.mp * d.np; g3.outT_ld = d.np;
@@ -528,7 +579,7 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
       g3.outT = outp; g3.outT_bs = (long long)d.n * d.m; g3.outT_ld = d.n;
       g3.valid_i = d.n; g3.valid_j = d.m;
     }
-    if ((rc = launch_gemm<EPI_AXPY>(g3, batch, stream, "ns K3 (aT + TB)"))) return rc;
+    if ((rc = launch_gemm<EPI_STORE>(g3, batch, stream, "ns K3 (T B')"))) return rc;
     bf16* t = Tc; Tc = Tn; Tn = t;
     t = Wc; Wc = Wn; Wn = t;
   }
