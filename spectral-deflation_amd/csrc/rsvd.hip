@@ -321,12 +321,29 @@ __global__ __launch_bounds__(256) void right_mult(const float* __restrict__ Y, i
 }
 
 // ---------------------------------------------------------------------------
-// Eigen-decomposition of H = Bp Bp^T (r x r, fp64) by cyclic Jacobi with the
-// round-robin ordering (r/2 disjoint rotations per round), one wavefront per
-// matrix: the wave works wave-synchronously on H and V in LDS (LDS accesses of a
-// wave complete in order), so no workgroup barriers are needed.  A rotation is
-// skipped when |h_pq| <= 1e-12 sqrt(h_pp h_qq) or |h_pq| <= 1e-15 trace(H); a
-// sweep without rotations ends the iteration.  Then the gate.
+// Eigen-decomposition of H = Bp Bp^T (r x r, fp64) by parallel cyclic Jacobi
+// (round-robin ordering: RP/2 disjoint rotations per round, all pairs once per
+// sweep of RP-1 rounds), one 256-thread workgroup per matrix.
+//
+// Storage order.  H and V are kept permuted so that every round rotates the
+// fixed pairs (2t, 2t+1): with the tournament schedule "position 0 stays, the
+// others move one seat", the positions of round rd+1 are those of round rd
+// taken through a fixed permutation sigma, applied while the rotated matrix is
+// written to the other buffer:  H <- Pi^T (J^T H J) Pi,  V <- V J Pi.  The
+// invariant H = V^T H0 V holds throughout, so at the end diag(H) are the
+// eigenvalues and the columns of V (original coordinates) their eigenvectors;
+// perm[] tracks the original index of each position (rows/columns >= r are
+// zero padding and never rotate).  All addresses are then fixed per thread.
+//
+// One round, one barrier: every wave computes all 32 angles itself from the
+// current buffer (identical results), then the workgroup writes the next
+// buffer: the 2x2 blocks (t, u), t <= u, as R_t^T X R_u (diagonal blocks by the
+// Golub-Van Loan update h_pp -= tan h_pq, h_qq += tan h_pq, h_pq = 0), and V's
+// column pairs.  Every round moves the seats, rotating or not, so that each
+// sweep visits every pair.  A pair is not rotated when h_pq^2 <= 1e-24 |h_pp h_qq|
+// or |h_pq| <= 1e-15 trace(H); after each sweep the whole of H is checked
+// against the same test, and the iteration ends when no pair passes it.  Then
+// the gate.
 // Outputs per matrix: s (descending, fp32), Ub (RP x RP: column t = eigenvector
 // of s_t), UbS = Ub diag(1/s) (for V = Bp^T Ub / s), the deflation width k and
 // the deflate / restore weights cw[t] = s_t h_t, cr[t] = h_t / pad.
@@ -336,178 +353,272 @@ struct GateParams {
   float ratio, thresh, pad;
 };
 
-constexpr int JP = RP + 1;   // LDS pitch: column walks hit distinct banks
+constexpr int JP = RP + 1;   // LDS pitch
 constexpr int NPAIR = RP / 2;
+constexpr int EG_THREADS = 256;
+constexpr int EG_BLOCKS = NPAIR * (NPAIR + 1) / 2;   // 2x2 blocks (t <= u)
 
-__device__ __forceinline__ double bcast_lane(double v, int lane) {
-  const long long bits = __double_as_longlong(v);
-  const int lo = __builtin_amdgcn_readlane((int)(bits & 0xffffffffLL), lane);
-  const int hi = __builtin_amdgcn_readlane((int)(bits >> 32), lane);
-  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+// next-round position of the element at position x (inverse of the seat move)
+__device__ __forceinline__ int jac_next(int x) {
+  if (x == 0) return 0;
+  if (x == 2) return 1;
+  if (x == RP - 1) return RP - 2;
+  return (x & 1) ? x + 2 : x - 2;
 }
 
-__global__ __launch_bounds__(64) void eig_gate(const double* __restrict__ part, GateParams gp,
-                                               const int* __restrict__ degen,
-                                               float* __restrict__ s_out, int s_ld,
-                                               float* __restrict__ Ub, float* __restrict__ UbS,
-                                               long long* __restrict__ k_out,
-                                               int* __restrict__ k_int,
-                                               float* __restrict__ cw, float* __restrict__ cr,
-                                               const double* __restrict__ qpart,
-                                               const double* __restrict__ asq, int asq_n,
-                                               float* __restrict__ d_out) {
-  // The whole RP x RP problem is rotated (rows/columns >= r are zero and never
-  // rotate), so the pair schedule is a compile-time 32 pairs x 63 rounds.
-  __shared__ double H[RP * JP];
-  __shared__ float V[RP * JP];        // eigenvectors (accumulated rotations), fp32
+// 1/sqrt(x) and 1/x in fp64 from the hardware estimates plus Newton steps
+// (relative error ~1e-16 for the positive normal arguments used here)
+__device__ __forceinline__ double rsqrt_nr(double x) {
+  double y = __builtin_amdgcn_rsq(x);
+  y = y * (1.5 - 0.5 * x * y * y);
+  y = y * (1.5 - 0.5 * x * y * y);
+  return y;
+}
+__device__ __forceinline__ double rcp_nr(double x) {
+  double y = __builtin_amdgcn_rcp(x);
+  y = y * (2.0 - x * y);
+  y = y * (2.0 - x * y);
+  return y;
+}
+
+__global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict__ part,
+                                                       GateParams gp,
+                                                       const int* __restrict__ degen,
+                                                       float* __restrict__ s_out, int s_ld,
+                                                       float* __restrict__ Ub,
+                                                       float* __restrict__ UbS,
+                                                       long long* __restrict__ k_out,
+                                                       int* __restrict__ k_int,
+                                                       float* __restrict__ cw,
+                                                       float* __restrict__ cr,
+                                                       const double* __restrict__ qpart,
+                                                       const double* __restrict__ asq, int asq_n,
+                                                       float* __restrict__ d_out) {
+  __shared__ double Hs[2][RP * JP];
+  __shared__ float Vs[2][RP * JP];        // eigenvectors (accumulated rotations), fp32
+  __shared__ double ang[4][3][NPAIR];     // per-wave copy of the round's cos, sin, tan
+  __shared__ int perm[2][RP];             // original index of each position
+  __shared__ double s_tr;
   __shared__ int order[RP];
   __shared__ float sv[RP];
-  const int b = blockIdx.x, l = threadIdx.x;
+  const int b = blockIdx.x, tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   const int r = gp.r;
   {
     const double* pb = part + (long long)b * GRAM_CHUNKS * RP * RP;
-    for (int e = l; e < RP * RP; e += 64) {
+    for (int e = tid; e < RP * RP; e += EG_THREADS) {
       const int i = e / RP, j = e % RP;
       double acc = 0.0;
 #pragma unroll
       for (int c = 0; c < GRAM_CHUNKS; ++c) acc += pb[(long long)c * RP * RP + e];
-      H[i * JP + j] = (i < r && j < r) ? acc : 0.0;
-      V[i * JP + j] = (i == j) ? 1.f : 0.f;
+      Hs[0][i * JP + j] = (i < r && j < r) ? acc : 0.0;
+      Vs[0][i * JP + j] = (i == j) ? 1.f : 0.f;
     }
+    if (tid < RP) perm[0][tid] = tid;
   }
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
   // absolute floor for |h_pq| (trace H = sum of the eigenvalues, invariant): off-
   // diagonals at rounding level relative to the largest eigenvalue stop rotating,
   // which guarantees the sweeps end
-  double tr = (l < r) ? fabs(H[l * JP + l]) : 0.0;
+  if (wave == 0) {
+    double tr = (l < r) ? fabs(Hs[0][l * JP + l]) : 0.0;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) tr += __shfl_xor(tr, o);
-  const double floor_pq = 1e-15 * tr;
+    for (int o = 32; o > 0; o >>= 1) tr += __shfl_xor(tr, o);
+    if (l == 0) s_tr = tr;
+  }
+  __syncthreads();
+  const double floor_pq = 1e-15 * s_tr;
 
+  // this thread's 2x2 blocks: blk -> (t, u), t <= u; read offsets (current
+  // buffer) and write offsets (next buffer, through the seat move)
+  int nb = 0;
+  int ro[3][4], wo[3][4], bt[3], bu[3];
+#pragma unroll
+  for (int x = 0; x < 3; ++x) {
+    const int blk = tid + EG_THREADS * x;
+    bt[x] = bu[x] = 0;
+#pragma unroll
+    for (int y = 0; y < 4; ++y) ro[x][y] = wo[x][y] = 0;
+    if (blk < EG_BLOCKS) {
+      int u = (int)((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
+      while ((u + 1) * (u + 2) / 2 <= blk) ++u;
+      while (u * (u + 1) / 2 > blk) --u;
+      const int t = blk - u * (u + 1) / 2;
+      bt[x] = t; bu[x] = u;
+      const int p = 2 * t, q = 2 * t + 1, p2 = 2 * u, q2 = 2 * u + 1;
+      ro[x][0] = p * JP + p2; ro[x][1] = p * JP + q2; ro[x][2] = q * JP + p2; ro[x][3] = q * JP + q2;
+      const int np_ = jac_next(p), nq = jac_next(q), np2 = jac_next(p2), nq2 = jac_next(q2);
+      wo[x][0] = np_ * JP + np2; wo[x][1] = np_ * JP + nq2; wo[x][2] = nq * JP + np2; wo[x][3] = nq * JP + nq2;
+      nb = x + 1;
+    }
+  }
+  // V items: row vrow, pairs vt0 + 4k, k < 8
+  const int vrow = tid & 63, vt0 = tid >> 6;
+  const int vrd = vrow * JP;
+  int vwp[NPAIR / 4], vwq[NPAIR / 4];
+#pragma unroll
+  for (int k = 0; k < NPAIR / 4; ++k) {
+    const int t = vt0 + 4 * k;
+    vwp[k] = vrd + jac_next(2 * t);
+    vwq[k] = vrd + jac_next(2 * t + 1);
+  }
+
+  int cur = 0;
   for (int sweep = 0; sweep < 40; ++sweep) {
-    bool rotated = false;
     for (int rd = 0; rd < RP - 1; ++rd) {
-      // lane t < 32 decides the rotation of pair t (circle method, position 0 fixed)
-      double c = 1.0, sn = 0.0;
+      const double* Hc = Hs[cur];
+      // angles of the round (every wave, lanes 0..31: pair t = lane)
       if (l < NPAIR) {
-        const int x1 = RP - 1 - l;
-        int p = l == 0 ? 0 : 1 + (l - 1 + rd) % (RP - 1);
-        int q = 1 + (x1 - 1 + rd) % (RP - 1);
-        if (p > q) { const int t = p; p = q; q = t; }
-        const double hpq = H[p * JP + q];
-        const double hpp = H[p * JP + p], hqq = H[q * JP + q];
-        if (fabs(hpq) > 1e-12 * sqrt(fabs(hpp * hqq)) && fabs(hpq) > floor_pq) {
-          const double theta = (hqq - hpp) / (2.0 * hpq);
-          const double t = (theta >= 0 ? 1.0 : -1.0) / (fabs(theta) + sqrt(1.0 + theta * theta));
-          c = 1.0 / sqrt(1.0 + t * t);
-          sn = t * c;
+        const double hpp = Hc[(2 * l) * JP + 2 * l], hpq = Hc[(2 * l) * JP + 2 * l + 1];
+        const double hqq = Hc[(2 * l + 1) * JP + 2 * l + 1];
+        double c = 1.0, sn = 0.0, tn = 0.0;
+        if (hpq * hpq > 1e-24 * fabs(hpp * hqq) && fabs(hpq) > floor_pq) {
+          const double theta = (hqq - hpp) * (0.5 * rcp_nr(hpq));
+          const double th2 = theta * theta;
+          // |theta| + sqrt(1 + theta^2)
+          const double den = fabs(theta) + (1.0 + th2) * rsqrt_nr(1.0 + th2);
+          tn = (theta >= 0 ? 1.0 : -1.0) * rcp_nr(den);
+          c = rsqrt_nr(1.0 + tn * tn);
+          sn = tn * c;
+        }
+        ang[wave][0][l] = c;
+        ang[wave][1][l] = sn;
+        ang[wave][2][l] = tn;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's angles are in LDS
+      double* Hn = Hs[cur ^ 1];
+      const float* Vc = Vs[cur];
+      float* Vn = Vs[cur ^ 1];
+      // loads first (H blocks, V pairs, angles), then the arithmetic and stores
+      double xv[3][4], a_c[3][2], a_s[3][2], a_t[3];
+#pragma unroll
+      for (int x = 0; x < 3; ++x) {
+        if (x < nb) {
+#pragma unroll
+          for (int y = 0; y < 4; ++y) xv[x][y] = Hc[ro[x][y]];
+          a_c[x][0] = ang[wave][0][bt[x]]; a_s[x][0] = ang[wave][1][bt[x]];
+          a_c[x][1] = ang[wave][0][bu[x]]; a_s[x][1] = ang[wave][1][bu[x]];
+          a_t[x] = ang[wave][2][bt[x]];
         }
       }
-      if (!__ballot(sn != 0.0)) continue;
-      rotated = true;
-      double cs[NPAIR], ss[NPAIR];
-      int ps[NPAIR], qs[NPAIR];
+      float vp[NPAIR / 4], vq[NPAIR / 4], vc[NPAIR / 4], vs[NPAIR / 4];
 #pragma unroll
-      for (int t = 0; t < NPAIR; ++t) {
-        cs[t] = bcast_lane(c, t);
-        ss[t] = bcast_lane(sn, t);
-        const int x1 = RP - 1 - t;
-        int p = t == 0 ? 0 : 1 + (t - 1 + rd) % (RP - 1);
-        int q = 1 + (x1 - 1 + rd) % (RP - 1);
-        ps[t] = p < q ? p : q;
-        qs[t] = p < q ? q : p;
+      for (int k = 0; k < NPAIR / 4; ++k) {
+        const int t = vt0 + 4 * k;
+        vp[k] = Vc[vrd + 2 * t];
+        vq[k] = Vc[vrd + 2 * t + 1];
+        vc[k] = (float)ang[wave][0][t];
+        vs[k] = (float)ang[wave][1][t];
       }
-      // rows: H <- J^T H  (lane = column); all loads first, then all stores
-      {
-        double hp[NPAIR], hq[NPAIR];
 #pragma unroll
-        for (int t = 0; t < NPAIR; ++t) { hp[t] = H[ps[t] * JP + l]; hq[t] = H[qs[t] * JP + l]; }
-#pragma unroll
-        for (int t = 0; t < NPAIR; ++t) {
-          H[ps[t] * JP + l] = cs[t] * hp[t] - ss[t] * hq[t];
-          H[qs[t] * JP + l] = ss[t] * hp[t] + cs[t] * hq[t];
+      for (int x = 0; x < 3; ++x) {
+        if (x < nb) {
+          double z00, z01, z10, z11;
+          if (bt[x] == bu[x]) {
+            // xv = [[h_pp, h_pq], [h_qp, h_qq]]
+            z00 = xv[x][0] - a_t[x] * xv[x][1];
+            z11 = xv[x][3] + a_t[x] * xv[x][1];
+            z01 = z10 = a_t[x] == 0.0 ? xv[x][1] : 0.0;   // unrotated pairs keep h_pq
+          } else {
+            const double c1 = a_c[x][0], s1 = a_s[x][0], c2 = a_c[x][1], s2 = a_s[x][1];
+            // rows: R_t^T X, then columns: (R_t^T X) R_u
+            const double y00 = c1 * xv[x][0] - s1 * xv[x][2], y01 = c1 * xv[x][1] - s1 * xv[x][3];
+            const double y10 = s1 * xv[x][0] + c1 * xv[x][2], y11 = s1 * xv[x][1] + c1 * xv[x][3];
+            z00 = c2 * y00 - s2 * y01; z01 = s2 * y00 + c2 * y01;
+            z10 = c2 * y10 - s2 * y11; z11 = s2 * y10 + c2 * y11;
+          }
+          Hn[wo[x][0]] = z00; Hn[wo[x][1]] = z01; Hn[wo[x][2]] = z10; Hn[wo[x][3]] = z11;
+          if (bt[x] != bu[x]) {   // mirror: (row, col) -> (col, row) in the next buffer
+            const int w00 = wo[x][0], w01 = wo[x][1], w10 = wo[x][2], w11 = wo[x][3];
+            Hn[(w00 % JP) * JP + w00 / JP] = z00;
+            Hn[(w01 % JP) * JP + w01 / JP] = z01;
+            Hn[(w10 % JP) * JP + w10 / JP] = z10;
+            Hn[(w11 % JP) * JP + w11 / JP] = z11;
+          }
         }
       }
-      __builtin_amdgcn_wave_barrier();
-      // columns: H <- H J, V <- V J  (lane = row)
-      {
-        double hp[NPAIR], hq[NPAIR];
 #pragma unroll
-        for (int t = 0; t < NPAIR; ++t) { hp[t] = H[l * JP + ps[t]]; hq[t] = H[l * JP + qs[t]]; }
-#pragma unroll
-        for (int t = 0; t < NPAIR; ++t) {
-          H[l * JP + ps[t]] = cs[t] * hp[t] - ss[t] * hq[t];
-          H[l * JP + qs[t]] = ss[t] * hp[t] + cs[t] * hq[t];
-        }
+      for (int k = 0; k < NPAIR / 4; ++k) {
+        Vn[vwp[k]] = vc[k] * vp[k] - vs[k] * vq[k];
+        Vn[vwq[k]] = vs[k] * vp[k] + vc[k] * vq[k];
       }
-      {
-        float vp[NPAIR], vq[NPAIR];
-#pragma unroll
-        for (int t = 0; t < NPAIR; ++t) { vp[t] = V[l * JP + ps[t]]; vq[t] = V[l * JP + qs[t]]; }
-#pragma unroll
-        for (int t = 0; t < NPAIR; ++t) {
-          const float cf = (float)cs[t], sf = (float)ss[t];
-          V[l * JP + ps[t]] = cf * vp[t] - sf * vq[t];
-          V[l * JP + qs[t]] = sf * vp[t] + cf * vq[t];
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
+      if (tid < RP) perm[cur ^ 1][jac_next(tid)] = perm[cur][tid];
+      __syncthreads();
+      cur ^= 1;
     }
-    if (!rotated) break;
+    // converged when no off-diagonal entry would still rotate
+    const double* Hc = Hs[cur];
+    int live = 0;
+    for (int e = tid; e < RP * RP; e += EG_THREADS) {
+      const int i = e / RP, j = e % RP;
+      if (i < j) {
+        const double h = Hc[i * JP + j];
+        live |= h * h > 1e-24 * fabs(Hc[i * JP + i] * Hc[j * JP + j]) && fabs(h) > floor_pq;
+      }
+    }
+    if (!__syncthreads_or(live)) break;
   }
-  // sort eigenvalues descending (stable rank; NaN ranks last)
-  order[l] = l;
-  __builtin_amdgcn_wave_barrier();
-  if (l < r) {
-    const double li = isnan(H[l * JP + l]) ? -INFINITY : H[l * JP + l];
+  const double* H = Hs[cur];
+  const float* V = Vs[cur];
+  const int* pm = perm[cur];
+  __syncthreads();
+  // sort eigenvalues descending over the real positions (original index < r;
+  // stable rank; NaN ranks last)
+  if (tid < RP) {
+    const bool real = pm[tid] < r;
+    const double li = isnan(H[tid * JP + tid]) ? -INFINITY : H[tid * JP + tid];
     int rank = 0;
-    for (int j = 0; j < r; ++j) {
+    for (int j = 0; j < RP; ++j) {
+      if (pm[j] >= r) continue;
       const double lj = isnan(H[j * JP + j]) ? -INFINITY : H[j * JP + j];
-      rank += (lj > li) || (lj == li && j < l);
+      rank += (lj > li) || (lj == li && j < tid);
     }
-    order[rank] = l;
+    if (real) order[rank] = tid;
   }
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
   const bool bad = degen && degen[b];
-  {
+  if (tid < RP) {
     float sval = 0.f;
-    if (l < r && !bad) {
-      const double ev = H[order[l] * JP + order[l]];
+    if (tid < r && !bad) {
+      const double ev = H[order[tid] * JP + order[tid]];
       sval = (float)sqrt(ev > 0.0 ? ev : 0.0);
     }
-    sv[l] = sval;
+    sv[tid] = sval;
   }
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
   // gate, fp32 comparisons as torch does them (deflation_batched.py:177-180)
   const float s0 = sv[0];
   const float thr = gp.thresh * s0;
-  const int kr = (int)__popcll(__ballot(l < r && sv[l] > thr));
+  int kr = 0;
+  for (int j = 0; j < r; ++j) kr += sv[j] > thr;
   const bool fired = (sv[gp.kw - 1] < gp.ratio * s0) && kr >= 1 && kr < r;
   const int kk = kr < 1 ? 1 : (kr > r - 1 ? r - 1 : kr);
-  if (l == 0) {
+  if (tid == 0) {
     k_out[b] = fired ? (long long)kk : 0LL;
     k_int[b] = fired ? kk : 0;
   }
-  if (l < r) s_out[(long long)b * s_ld + l] = sv[l];
-  const float h = (fired && l < kk) ? 1.f : 0.f;
-  cw[(long long)b * RP + l] = sv[l] * h;
-  cr[(long long)b * RP + l] = h * (1.0f / gp.pad);
+  if (tid < RP) {
+    if (tid < r) s_out[(long long)b * s_ld + tid] = sv[tid];
+    const float h = (fired && tid < kk) ? 1.f : 0.f;
+    cw[(long long)b * RP + tid] = sv[tid] * h;
+    cr[(long long)b * RP + tid] = h * (1.0f / gp.pad);
+  }
   float* Ubb = Ub + (long long)b * RP * RP;
   float* UbSb = UbS + (long long)b * RP * RP;
-  for (int e = l; e < RP * RP; e += 64) {
+  for (int e = tid; e < RP * RP; e += EG_THREADS) {
     const int a = e / RP, t = e % RP;   // row a of Ub, column t (sorted)
     float u = 0.f;
     if (a < r && t < r && !bad) u = V[a * JP + order[t]];
     Ubb[e] = u;
     UbSb[e] = sv[t] > 0.f ? u / sv[t] : 0.f;
   }
-  if (!d_out) return;
+  if (!d_out || wave != 0) return;
   // ||W||_F^2 for W = A - sum_{t<k} s_t U_t V_t^T with U_t = Q Ub_t, V_t = Bp^T Ub_t / s_t:
   //   <A, U_t V_t^T> = Ub_t^T (Q^T A)(A^T Q) Ub_t / s_t = lambda_t / s_t,
   //   V_t^T V_t' = delta_tt' lambda_t / s_t^2,  U_t^T U_t = Ub_t^T (Q^T Q) Ub_t = G_t,
   // so ||W||^2 = ||A||^2 - sum_{t<k} lambda_t (2 - G_t).  Q^T Q is kept (not assumed
   // to be I): single-pass CholeskyQR in fp32 leaves it ~kappa*eps off the identity,
-  // and the reference's explicit W sees the same Q.
+  // and the reference's explicit W sees the same Q.  (Wave 0 only; the spare H
+  // buffer is no longer read by the other waves, which have left.)
   double asum = 0.0;
   for (int i = l; i < asq_n; i += 64) asum += asq[(long long)b * asq_n + i];
 #pragma unroll
@@ -516,14 +627,15 @@ __global__ __launch_bounds__(64) void eig_gate(const double* __restrict__ part, 
   if (fired) {
     const double lam_l = (l < r) ? H[order[l] * JP + order[l]] : 0.0;   // lambda of rank l
     __builtin_amdgcn_wave_barrier();
-    // reuse H for Q^T Q
+    // Q^T Q into the free buffer
+    double* G = Hs[cur ^ 1];
     const double* qb = qpart + (long long)b * GRAM_CHUNKS * RP * RP;
     for (int e = l; e < RP * RP; e += 64) {
       const int i = e / RP, j = e % RP;
       double acc = 0.0;
 #pragma unroll
       for (int c = 0; c < GRAM_CHUNKS; ++c) acc += qb[(long long)c * RP * RP + e];
-      H[i * JP + j] = (i < r && j < r) ? acc : 0.0;
+      G[i * JP + j] = (i < r && j < r) ? acc : 0.0;
     }
     __builtin_amdgcn_wave_barrier();
     double head = 0.0;
@@ -531,7 +643,7 @@ __global__ __launch_bounds__(64) void eig_gate(const double* __restrict__ part, 
       const int ct = order[t];
       double y = 0.0;                       // (Q^T Q Ub_t)_l
       if (l < r)
-        for (int c = 0; c < r; ++c) y = fma(H[l * JP + c], (double)V[c * JP + ct], y);
+        for (int c = 0; c < r; ++c) y = fma(G[l * JP + c], (double)V[c * JP + ct], y);
       double gt = (l < r) ? (double)V[l * JP + ct] * y : 0.0;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) gt += __shfl_xor(gt, o);
@@ -791,7 +903,7 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
     return rc;
   if ((rc = gram(st, w.Bt, B, m, w.gram))) return rc;
   if (d && (rc = gram(st, w.Q, B, n, w.gramq))) return rc;
-  hipLaunchKernelGGL(eig_gate, dim3(B), dim3(64), 0, st, w.gram, gp, w.degen, w.s, RP, w.Ub,
+  hipLaunchKernelGGL(eig_gate, dim3(B), dim3(EG_THREADS), 0, st, w.gram, gp, w.degen, w.s, RP, w.Ub,
                      w.UbS, k_out, w.kint, w.cw, w.cr, d ? w.gramq : nullptr,
                      d ? w.asq : nullptr, ceil_div(n, SG_ROWS), d);
   DMH_CHECK_LAUNCH("eig_gate");
@@ -915,7 +1027,7 @@ int dmh_project(hipStream_t stream, const float* Q, const float* A, int batch, i
   if (rc) return rc;
   if ((rc = gram(stream, w.Bt, batch, m, w.gram))) return rc;
   GateParams gp{r, 1, 0.f, 0.f, 1.f};
-  hipLaunchKernelGGL(eig_gate, dim3(batch), dim3(64), 0, stream, w.gram, gp, w.degen, w.s, RP,
+  hipLaunchKernelGGL(eig_gate, dim3(batch), dim3(EG_THREADS), 0, stream, w.gram, gp, w.degen, w.s, RP,
                      w.Ub, w.UbS, w.k64, w.kint, w.cw, w.cr, (const double*)nullptr,
                      (const double*)nullptr, 0, (float*)nullptr);
   DMH_CHECK_LAUNCH("eig_gate");
