@@ -665,6 +665,17 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
 //        outside n x m), so the chain can start without its entry pass
 // ---------------------------------------------------------------------------
 constexpr int DR_ROWS = 64, DR_COLS = 128;
+constexpr int DR_KC = 16;   // head columns staged per chunk
+
+// LDS of one restore tile: the head chunk (U rows of the tile, V rows of the tile
+// transposed) while the rank-k update runs, then the bf16 tile of W = T^T.
+union RestoreLds {
+  struct {
+    float Us[DR_ROWS][DR_KC + 1];        // U[i][t0 + t]
+    float Vt[DR_KC][DR_COLS + 4];        // V[j][t0 + t] as Vt[t][j]
+  } head;
+  bf16 tw[DR_COLS][DR_ROWS + 8];         // tile of W = T^T
+};
 
 __global__ __launch_bounds__(256) void deflate_restore(
     const float* __restrict__ A, int n, int m, const float* __restrict__ U,
@@ -672,61 +683,65 @@ __global__ __launch_bounds__(256) void deflate_restore(
     const float* __restrict__ cr, const float* __restrict__ dvec, void* __restrict__ X0,
     int x0_mode /*0 none, 1 bf16, 2 fp32*/, bf16* __restrict__ T, bf16* __restrict__ W, int np,
     int mp) {
-  __shared__ __attribute__((aligned(16))) float Us[DR_ROWS][RP + 1];   // U[i][t], tile rows
-  __shared__ __attribute__((aligned(16))) float Vt[RP][DR_COLS + 4];   // V[j][t] as Vt[t][j]
+  __shared__ __attribute__((aligned(16))) RestoreLds sm;
   __shared__ float coef[RP];
-  __shared__ __attribute__((aligned(16))) bf16 tw[DR_COLS][DR_ROWS + 8]; // tile of W = T^T
   const int b = blockIdx.z;
   const int i0 = blockIdx.y * DR_ROWS, j0 = blockIdx.x * DR_COLS;
   const int tid = threadIdx.x;
   const int k = kvec[b];
   const float d = dvec[b];
   const float* Ab = A + (long long)b * n * m;
-  const int k4 = (k + 3) >> 2;                      // float4 chunks of the head columns
-  for (int e = tid; e < DR_ROWS * 16; e += 256) {   // U rows
-    const int rr = e >> 4, t4 = e & 15;
-    const int gi = i0 + rr;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t4 < k4 && gi < n) v = *(const float4*)&U[((long long)b * n + gi) * RP + 4 * t4];
-    Us[rr][4 * t4] = v.x; Us[rr][4 * t4 + 1] = v.y; Us[rr][4 * t4 + 2] = v.z; Us[rr][4 * t4 + 3] = v.w;
-  }
-  for (int e = tid; e < DR_COLS * 16; e += 256) {   // V rows, transposed
-    const int cc = e >> 4, t4 = e & 15;
-    const int gj = j0 + cc;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t4 < k4 && gj < m) v = *(const float4*)&V[((long long)b * m + gj) * RP + 4 * t4];
-    Vt[4 * t4][cc] = v.x; Vt[4 * t4 + 1][cc] = v.y; Vt[4 * t4 + 2][cc] = v.z; Vt[4 * t4 + 3][cc] = v.w;
-  }
-  if (tid < RP) coef[tid] = cw[b * RP + tid] / d - cr[b * RP + tid];
-  __syncthreads();
   const int c4 = (tid & 31) * 4;      // 4 consecutive columns of the tile
   const int rw = tid >> 5;            // rows rw + 8a, a = 0..7
   const bool vec = (m & 3) == 0;
+  // A first (the bulk of the traffic), so its loads are in flight while the head
+  // coefficients and chunks are staged
   float x[8][4];
 #pragma unroll
   for (int a = 0; a < 8; ++a) {
     const int gi = i0 + rw + 8 * a, gj = j0 + c4;
     if (gi < n && vec && gj + 3 < m) {
       const float4 v = *(const float4*)&Ab[(long long)gi * m + gj];
-      x[a][0] = v.x / d; x[a][1] = v.y / d; x[a][2] = v.z / d; x[a][3] = v.w / d;
+      x[a][0] = v.x; x[a][1] = v.y; x[a][2] = v.z; x[a][3] = v.w;
     } else {
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        x[a][c] = (gi < n && gj + c < m) ? Ab[(long long)gi * m + gj + c] / d : 0.f;
+        x[a][c] = (gi < n && gj + c < m) ? Ab[(long long)gi * m + gj + c] : 0.f;
     }
   }
-  for (int t = 0; t < k; ++t) {
-    const float4 v = *(const float4*)&Vt[t][c4];
-    const float ct = coef[t];
+  if (tid < RP) coef[tid] = cw[b * RP + tid] / d - cr[b * RP + tid];
 #pragma unroll
-    for (int a = 0; a < 8; ++a) {
-      const float u = Us[rw + 8 * a][t] * ct;
-      x[a][0] = fmaf(-u, v.x, x[a][0]);
-      x[a][1] = fmaf(-u, v.y, x[a][1]);
-      x[a][2] = fmaf(-u, v.z, x[a][2]);
-      x[a][3] = fmaf(-u, v.w, x[a][3]);
+  for (int a = 0; a < 8; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[a][c] = x[a][c] / d;
+  for (int t0 = 0; t0 < k; t0 += DR_KC) {
+    const int kc = min(DR_KC, k - t0);
+    __syncthreads();   // coef visible; the previous chunk consumed
+    for (int e = tid; e < DR_ROWS * DR_KC; e += 256) {   // U rows
+      const int rr = e / DR_KC, t = e % DR_KC;
+      const int gi = i0 + rr;
+      sm.head.Us[rr][t] = (t < kc && gi < n) ? U[((long long)b * n + gi) * RP + t0 + t] : 0.f;
+    }
+    for (int e = tid; e < DR_COLS * DR_KC; e += 256) {   // V rows, transposed
+      const int cc = e / DR_KC, t = e % DR_KC;
+      const int gj = j0 + cc;
+      sm.head.Vt[t][cc] = (t < kc && gj < m) ? V[((long long)b * m + gj) * RP + t0 + t] : 0.f;
+    }
+    __syncthreads();
+    for (int t = 0; t < kc; ++t) {
+      const float4 v = *(const float4*)&sm.head.Vt[t][c4];
+      const float ct = coef[t0 + t];
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        const float u = sm.head.Us[rw + 8 * a][t] * ct;
+        x[a][0] = fmaf(-u, v.x, x[a][0]);
+        x[a][1] = fmaf(-u, v.y, x[a][1]);
+        x[a][2] = fmaf(-u, v.z, x[a][2]);
+        x[a][3] = fmaf(-u, v.w, x[a][3]);
+      }
     }
   }
+  if (W) __syncthreads();   // the head chunk is consumed before tw overwrites it
 #pragma unroll
   for (int a = 0; a < 8; ++a) {
     const int il = rw + 8 * a;
@@ -751,7 +766,7 @@ __global__ __launch_bounds__(256) void deflate_restore(
       *(bf16x4*)(T + (long long)b * np * mp + (long long)gi * mp + gj) = o;
     if (W) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) tw[c4 + c][il] = o[c];
+      for (int c = 0; c < 4; ++c) sm.tw[c4 + c][il] = o[c];
     }
   }
   if (W) {
@@ -761,7 +776,7 @@ __global__ __launch_bounds__(256) void deflate_restore(
       const int jj = e >> 3, ch = (e & 7) * 8;
       const int gj = j0 + jj, gi = i0 + ch;
       if (gj < mp && gi < np)
-        *(uint4*)(W + (long long)b * mp * np + (long long)gj * np + gi) = *(const uint4*)&tw[jj][ch];
+        *(uint4*)(W + (long long)b * mp * np + (long long)gj * np + gi) = *(const uint4*)&sm.tw[jj][ch];
     }
   }
 }
