@@ -63,7 +63,10 @@ constexpr int ROWB = TK * 2;                 // bytes per LDS row
 constexpr int OPB = TILE * ROWB;             // bytes per operand tile (16 KB)
 constexpr int STAGEB = 2 * OPB;              // P + Q
 constexpr int GEMM_THREADS = 256;
-static_assert(NSTAGE * STAGEB == 128 * 1024, "LDS ring must equal the epilogue tile");
+constexpr int RING_BYTES = NSTAGE * STAGEB > 128 * 1024 ? NSTAGE * STAGEB : 128 * 1024;
+static_assert(RING_BYTES <= 160 * 1024, "LDS ring and epilogue tile must fit the 160 KB of a CU");
+// loads of the stages younger than the one waited for (8 per stage per wave)
+constexpr int RING_VMCNT = 8 * (NSTAGE - 2);
 
 enum { EPI_STORE = 0, EPI_POLY = 1 };
 
@@ -118,7 +121,7 @@ __device__ __forceinline__ void ring_barrier() {
 template <int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_nt_bf16(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[NSTAGE * STAGEB];
+  __shared__ __attribute__((aligned(1024))) char smem[RING_BYTES];
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   int b, ti, tj;
@@ -175,19 +178,19 @@ void gemm_nt_bf16(GemmArgs g) {
   const int fch0 = ((0 + hi) ^ sw) * 16, fch1 = ((2 + hi) ^ sw) * 16;
 
   // Main loop, software-pipelined at two levels:
-  //  * LDS ring: stages kt+1..kt+3 are in flight while stage kt is consumed.  The
+  //  * LDS ring: stages kt+1..kt+NSTAGE-1 are in flight while stage kt is consumed.  The
   //    prefetch is unconditional: past the last stage it re-fetches the last stage
   //    into the free slot (never read), so every step waits on the same vmcnt and
   //    the loop body is one basic block the scheduler can interleave.
   //  * fragments: the k16 substep-0 fragments of stage kt+1 are read from LDS
   //    under the substep-1 MFMAs of stage kt, and substep 1 under substep 0, so the
   //    MFMA pipe never waits on LDS at the top of a step.
-  // Slot (kt+3)&3 refilled at step kt held stage kt-1, whose last fragment reads
+  // The slot refilled at step kt (stage kt+NSTAGE-1) held stage kt-1, whose last fragment reads
   // completed (lgkmcnt(0)) before the barrier of step kt-1.
   const int nk = g.K / TK;
 #pragma unroll
   for (int p = 0; p < NSTAGE - 1; ++p) DMH_GLOAD(min(p, nk - 1) * TK, p);
-  asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // stage 0 landed (own loads)
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");   // stage 0 landed (own loads)
   ring_barrier();                                       // ... and everyone's
 
   bf16x8 f0p[4], f0q[4], f1p[4], f1q[4];
@@ -196,15 +199,18 @@ void gemm_nt_bf16(GemmArgs g) {
     f0p[i] = *(const bf16x8*)(smem + fP + i * 32 * ROWB + fch0);
     f0q[i] = *(const bf16x8*)(smem + fQ + i * 32 * ROWB + fch0);
   }
+  int s_cur = 0;   // ring slot of stage kt
   for (int kt = 0; kt < nk; ++kt) {
-    const char* cur = smem + (kt & (NSTAGE - 1)) * STAGEB;
-    const char* nxt = smem + ((kt + 1) & (NSTAGE - 1)) * STAGEB;
+    const int s_nxt = s_cur + 1 == NSTAGE ? 0 : s_cur + 1;
+    const int s_pre = s_cur == 0 ? NSTAGE - 1 : s_cur - 1;   // slot of stage kt + NSTAGE - 1
+    const char* cur = smem + s_cur * STAGEB;
+    const char* nxt = smem + s_nxt * STAGEB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f1p[i] = *(const bf16x8*)(cur + fP + i * 32 * ROWB + fch1);
       f1q[i] = *(const bf16x8*)(cur + fQ + i * 32 * ROWB + fch1);
     }
-    DMH_GLOAD(min(kt + NSTAGE - 1, nk - 1) * TK, (kt + NSTAGE - 1) & (NSTAGE - 1));
+    DMH_GLOAD(min(kt + NSTAGE - 1, nk - 1) * TK, s_pre);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -220,9 +226,9 @@ void gemm_nt_bf16(GemmArgs g) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (direct-to-LDS prefetch)
     }
-    // stage kt+1 landed: the younger loads in flight are stages kt+2, kt+3 (8 per
-    // stage per wave), and loads retire in issue order
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    // stage kt+1 landed: the younger loads in flight are those of stages
+    // kt+2 .. kt+NSTAGE-1, and loads retire in issue order
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");
     ring_barrier();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -240,6 +246,7 @@ void gemm_nt_bf16(GemmArgs g) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (next substep-0 fragments)
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    s_cur = s_nxt;
   }
 #undef DMH_GLOAD
   // the re-fetches past the last stage may still be landing in LDS

@@ -1,0 +1,110 @@
+"""GPU parity at the full BASELINE.json shapes of configs 3 and 4.
+
+Config 3: GPT-2 small, one Muon polar step per arm over 48 x (768, 768) and
+24 x (3072, 768) tall matrices (12 layers x {3 QKV blocks, attn proj} and
+{c_fc, mlp proj^T}), 8 spikes 50x..10x over a Marchenko-Pastur bulk.
+Config 4: GPT-2 medium, deflated_pe_cut over 96 x (1024, 1024) and
+48 x (4096, 1024), 16 spikes 100x..5x (expected k = 12) with every 4th matrix
+left unspiked (expected k = 0).
+
+Every gate decision is checked exactly; the polar factors are checked against
+the oracle (same sketch, drawn with the reference's seed formula, muon.py:290-291)
+on a sample of matrices per group, with the tolerances of tests/parity.py.
+"""
+
+import pytest
+import torch
+
+from oracle import polar_oracle as O
+from parity import assert_polar_parity
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+SMALL = [(48, 768, 768), (24, 3072, 768)]
+MEDIUM = [(96, 1024, 1024), (48, 4096, 1024)]
+
+
+@pytest.fixture(scope="module")
+def mods():
+    from defmuon_amd import _native
+    from defmuon_amd import synthetic as S
+    from defmuon_amd.optim import deflation_cutoff as C
+    from defmuon_amd.optim import muon as M
+    from defmuon_amd.optim import polar_express as PE
+    _native.load()
+    return S, C, M, PE
+
+
+def _deflated_group(C, arm, A, gi, bd_step=1):
+    """One shape group through the arm's polar_group, with the sketch drawn the
+    way the optimizer draws it; returns (U, k, Omega)."""
+    fac = C.ARMS[arm]()
+    B, n, m = A.shape
+    r, _ = O.sketch_dims(m)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(O.group_seed(bd_step, gi))
+    Om = torch.randn(B, m, r, device=DEV, dtype=torch.float32, generator=gen)
+    U, k, _ = fac.polar_group(A, steps=5, Omega=Om)
+    torch.cuda.synchronize()
+    return U, k, Om
+
+
+def _check_deflated_sample(arm, A, Om, U, idx):
+    pad = O.DIVISOR_PAD if arm == "deflated_ns_cut" else O.PE_PAD
+    hs = O.ns_schedule(5) if arm == "deflated_ns_cut" else O.pe_schedule(5)
+    for i in idx:
+        Ai = A[i:i + 1].cpu()
+        X0, _, _ = O.rmfro_clip(Ai, Om[i:i + 1].cpu(), pad=pad, out_dtype=torch.bfloat16)
+        Uo = O.horner_iterate(X0, hs)
+        assert_polar_parity(U[i].cpu(), Uo[0], Ai[0], tag=f"{arm} {tuple(A.shape)} #{i}")
+
+
+@pytest.mark.parametrize("arm", ["deflated_ns_cut", "deflated_pe_cut"])
+def test_config3_gpt2_small_deflated(mods, arm):
+    S, C, _, _ = mods
+    for gi, (B, n, m) in enumerate(SMALL):
+        A = S.spiked_batch(B, n, m, seed=300 + gi, n_spikes=8, hi=50.0, lo=10.0, device=DEV)
+        U, k, Om = _deflated_group(C, arm, A, gi)
+        assert k.tolist() == [8] * B, k.tolist()
+        assert torch.isfinite(U.float()).all()
+        _check_deflated_sample(arm, A, Om, U, [0, B - 1])
+
+
+@pytest.mark.parametrize("arm", ["ns5", "polarexpress"])
+def test_config3_gpt2_small_plain(mods, arm):
+    """The plain arms run per parameter (muon.py:361-402): one GPT-2-small layer's
+    four parameters, in nn.Linear (out, in) layout, W_QKV as its (3, d, d) split."""
+    S, _, M, PE = mods
+    fn = M.zeropower_via_newtonschulz5 if arm == "ns5" else PE.PolarExpress
+    ofn = O.ns5 if arm == "ns5" else O.polar_express
+    d = 768
+    params = {
+        "attn.c_attn": S.spiked_batch(3, d, d, seed=31, device=DEV),
+        "attn.c_proj": S.spiked_batch(1, d, d, seed=32, device=DEV)[0],
+        "mlp.c_fc": S.spiked_batch(1, 4 * d, d, seed=33, device=DEV)[0],
+        "mlp.c_proj": S.spiked_batch(1, d, 4 * d, seed=34, device=DEV)[0],
+    }
+    for name, G in params.items():
+        u = fn(G, 5)
+        torch.cuda.synchronize()
+        assert u.shape == G.shape and u.dtype == torch.bfloat16
+        uo = ofn(G.cpu(), 5)
+        Gs = G if G.ndim == 3 else G[None]
+        us, uos = (u if u.ndim == 3 else u[None]), (uo if uo.ndim == 3 else uo[None])
+        for b in range(Gs.shape[0]):
+            assert_polar_parity(us[b].cpu(), uos[b], Gs[b].cpu(), tag=f"{arm} {name}[{b}]")
+
+
+def test_config4_gpt2_medium_pe(mods):
+    S, C, _, _ = mods
+    for gi, (B, n, m) in enumerate(MEDIUM):
+        unspiked = tuple(range(0, B, 4))
+        A = S.spiked_batch(B, n, m, seed=400 + gi, n_spikes=16, hi=100.0, lo=5.0,
+                           device=DEV, unspiked=unspiked)
+        U, k, Om = _deflated_group(C, "deflated_pe_cut", A, gi)
+        want = [0 if i in unspiked else S.expected_k(16, 100.0, 5.0) for i in range(B)]
+        assert want.count(12) == B - len(unspiked)
+        assert k.tolist() == want, k.tolist()
+        assert torch.isfinite(U.float()).all()
+        _check_deflated_sample("deflated_pe_cut", A, Om, U, [0, 1])
