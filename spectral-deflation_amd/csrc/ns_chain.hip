@@ -46,8 +46,9 @@ void set_error(const char* fmt, ...) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA GEMM tile: 256 x 256 output per workgroup, 4 waves of 128 x 128, K step 32,
-// a 4-stage LDS ring (three K steps of loads in flight while one is consumed).
+// MFMA GEMM tile: 256 x 256 output per workgroup, 8 waves (two per SIMD) of
+// 128 x 64, K step 32, a 4-stage LDS ring (three K steps of loads in flight
+// while one is consumed).
 //
 // Operand tiles go global -> LDS with the gfx950 direct-to-LDS load
 // (global_load_lds_dwordx4: lane L of a wave writes 16 bytes at base + 16 L, no
@@ -62,11 +63,18 @@ constexpr int NSTAGE = 4;
 constexpr int ROWB = TK * 2;                 // bytes per LDS row
 constexpr int OPB = TILE * ROWB;             // bytes per operand tile (16 KB)
 constexpr int STAGEB = 2 * OPB;              // P + Q
-constexpr int GEMM_THREADS = 256;
+// 8 waves, two per SIMD (so one wave's MFMAs fill the other's waits), as a
+// 2 x 4 grid of 128 x 64 wave tiles: 4 x 2 MFMA blocks of 32 x 32 per wave.
+constexpr int GEMM_WAVES = 8;
+constexpr int GEMM_THREADS = 64 * GEMM_WAVES;
+constexpr int WAVES_N = 4;                      // waves along the Q rows (output columns)
+constexpr int WT_M = TILE / (GEMM_WAVES / WAVES_N), WT_N = TILE / WAVES_N;
+constexpr int BM = WT_M / 32, BN = WT_N / 32;   // MFMA blocks per wave
+constexpr int LQ = TILE / GEMM_WAVES / 16;      // loads per operand per stage per lane
 constexpr int RING_BYTES = NSTAGE * STAGEB > 128 * 1024 ? NSTAGE * STAGEB : 128 * 1024;
 static_assert(RING_BYTES <= 160 * 1024, "LDS ring and epilogue tile must fit the 160 KB of a CU");
 // loads of the stages younger than the one waited for (8 per stage per wave)
-constexpr int RING_VMCNT = 8 * (NSTAGE - 2);
+constexpr int RING_VMCNT = 2 * LQ * (NSTAGE - 2);
 
 enum { EPI_STORE = 0, EPI_POLY = 1 };
 
@@ -119,7 +127,8 @@ __device__ __forceinline__ void ring_barrier() {
 }
 
 template <int EPI>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(GEMM_THREADS, GEMM_THREADS),
+                          amdgpu_waves_per_eu(GEMM_WAVES / 4, GEMM_WAVES / 4)))
 void gemm_nt_bf16(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char smem[RING_BYTES];
 
@@ -129,43 +138,52 @@ void gemm_nt_bf16(GemmArgs g) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   const bf16* P = g.P + (long long)b * g.p_bs + (long long)(ti * TILE) * g.p_ld;
   const bf16* Q = g.Q + (long long)b * g.q_bs + (long long)(tj * TILE) * g.q_ld;
 
-  // Loader: wave w, instruction q covers tile rows 64w + 16q .. +15; lane L fills
-  // slot L & 3 of row 64w + 16q + (L >> 2) with the global chunk slot ^ swz(row).
-  const int lrow0 = 64 * wave + (lane >> 2);
+  // Loader: buffer loads straight into LDS (buffer_load_dwordx4 ... lds).  Wave w,
+  // instruction q covers tile rows (TILE/GEMM_WAVES) w + 16q .. +15; lane L fills
+  // slot L & 3 of row (TILE/GEMM_WAVES) w + 16q + (L >> 2) with the global chunk
+  // slot ^ swz(row).  The per-lane byte
+  // offsets are fixed for the whole K loop, the K step goes into the scalar offset
+  // and the LDS destination (M0) is wave-uniform, so a load costs no VALU work.
+  const __amdgpu_buffer_rsrc_t rP =
+      __builtin_amdgcn_make_buffer_rsrc((void*)P, (short)0, TILE * g.p_ld * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rQ =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Q, (short)0, TILE * g.q_ld * 2, 0x00020000);
+  const int lrow0 = (TILE / GEMM_WAVES) * wave + (lane >> 2);
   const int lslot = lane & 3;
-  int goffP[4], goffQ[4];   // element offsets within the tile (32-bit)
+  int boffP[LQ], boffQ[LQ];   // byte offsets within the tile
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < LQ; ++q) {
     const int r = lrow0 + 16 * q;
     const int c = lslot ^ lds_swz(r);
-    goffP[q] = r * g.p_ld + c * 8;
-    goffQ[q] = r * g.q_ld + c * 8;
+    boffP[q] = (r * g.p_ld + c * 8) * 2;
+    boffQ[q] = (r * g.q_ld + c * 8) * 2;
   }
-  char* const lds_wave = smem + wave * 64 * ROWB;   // this wave's first row in each tile
+  char* const lds_wave = smem + wave * (TILE / GEMM_WAVES) * ROWB;   // this wave's first row
 
 #define DMH_GLOAD(k0, st)                                                              \
   do {                                                                                 \
     char* dP = lds_wave + (st) * STAGEB;                                               \
     char* dQ = dP + OPB;                                                               \
-    _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                    \
-      __builtin_amdgcn_global_load_lds((const void*)(P + (k0) + goffP[q]),             \
-                                       (lds_ptr_t)(dP + q * 16 * ROWB), 16, 0, 0);     \
-      __builtin_amdgcn_global_load_lds((const void*)(Q + (k0) + goffQ[q]),             \
-                                       (lds_ptr_t)(dQ + q * 16 * ROWB), 16, 0, 0);     \
+    const int so = (k0) * 2;                                                           \
+    _Pragma("unroll") for (int q = 0; q < LQ; ++q) {                                   \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_ptr_t)(dP + q * 16 * ROWB), 16, \
+                                               boffP[q], so, 0, 0);                    \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_ptr_t)(dQ + q * 16 * ROWB), 16, \
+                                               boffQ[q], so, 0, 0);                    \
     }                                                                                  \
   } while (0)
 
-  f32x16 acc[4][4];
+  f32x16 acc[BM][BN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < BM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < BN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
@@ -173,8 +191,8 @@ void gemm_nt_bf16(GemmArgs g) {
   const int hi = lane >> 5;
   const int sw = lds_swz(r32);
   // byte offsets of this lane's fragment rows (row 32i + r32 of the wave's half)
-  const int fP = (128 * wm + r32) * ROWB;
-  const int fQ = OPB + (128 * wn + r32) * ROWB;
+  const int fP = (WT_M * wm + r32) * ROWB;
+  const int fQ = OPB + (WT_N * wn + r32) * ROWB;
   const int fch0 = ((0 + hi) ^ sw) * 16, fch1 = ((2 + hi) ^ sw) * 16;
 
   // Main loop, software-pipelined at two levels:
@@ -193,12 +211,11 @@ void gemm_nt_bf16(GemmArgs g) {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");   // stage 0 landed (own loads)
   ring_barrier();                                       // ... and everyone's
 
-  bf16x8 f0p[4], f0q[4], f1p[4], f1q[4];
+  bf16x8 f0p[BM], f0q[BN], f1p[BM], f1q[BN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f0p[i] = *(const bf16x8*)(smem + fP + i * 32 * ROWB + fch0);
-    f0q[i] = *(const bf16x8*)(smem + fQ + i * 32 * ROWB + fch0);
-  }
+  for (int i = 0; i < BM; ++i) f0p[i] = *(const bf16x8*)(smem + fP + i * 32 * ROWB + fch0);
+#pragma unroll
+  for (int j = 0; j < BN; ++j) f0q[j] = *(const bf16x8*)(smem + fQ + j * 32 * ROWB + fch0);
   int s_cur = 0;   // ring slot of stage kt
   for (int kt = 0; kt < nk; ++kt) {
     const int s_nxt = s_cur + 1 == NSTAGE ? 0 : s_cur + 1;
@@ -206,23 +223,23 @@ void gemm_nt_bf16(GemmArgs g) {
     const char* cur = smem + s_cur * STAGEB;
     const char* nxt = smem + s_nxt * STAGEB;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f1p[i] = *(const bf16x8*)(cur + fP + i * 32 * ROWB + fch1);
-      f1q[i] = *(const bf16x8*)(cur + fQ + i * 32 * ROWB + fch1);
-    }
+    for (int i = 0; i < BM; ++i) f1p[i] = *(const bf16x8*)(cur + fP + i * 32 * ROWB + fch1);
+#pragma unroll
+    for (int j = 0; j < BN; ++j) f1q[j] = *(const bf16x8*)(cur + fQ + j * 32 * ROWB + fch1);
     DMH_GLOAD(min(kt + NSTAGE - 1, nk - 1) * TK, s_pre);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < BM; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < BN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0q[j], f0p[i], acc[i][j], 0, 0, 0);
+    // interleave: substep-1 fragment reads, then the prefetch loads, among the MFMAs
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
+    for (int x = 0; x < BM + BN; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (substep-1 fragments)
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     }
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
+    for (int x = 0; x < 2 * LQ; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (direct-to-LDS prefetch)
     }
@@ -231,21 +248,20 @@ void gemm_nt_bf16(GemmArgs g) {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");
     ring_barrier();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f0p[i] = *(const bf16x8*)(nxt + fP + i * 32 * ROWB + fch0);
-      f0q[i] = *(const bf16x8*)(nxt + fQ + i * 32 * ROWB + fch0);
-    }
+    for (int i = 0; i < BM; ++i) f0p[i] = *(const bf16x8*)(nxt + fP + i * 32 * ROWB + fch0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < BN; ++j) f0q[j] = *(const bf16x8*)(nxt + fQ + j * 32 * ROWB + fch0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+    for (int i = 0; i < BM; ++i)
+#pragma unroll
+      for (int j = 0; j < BN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1q[j], f1p[i], acc[i][j], 0, 0, 0);
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
+    for (int x = 0; x < BM + BN; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (next substep-0 fragments)
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, BM * BN - (BM + BN), 0);
     s_cur = s_nxt;
   }
 #undef DMH_GLOAD
@@ -266,11 +282,12 @@ void gemm_nt_bf16(GemmArgs g) {
   // The barriers below only order LDS (lgkmcnt), so the aux tile, fetched in one
   // batch up front, stays in flight while the accumulators drain.
   const int gi0 = ti * TILE, gj0 = tj * TILE;
-  bf16x8 av[32];
+  constexpr int NU = TILE * TILE / 8 / GEMM_THREADS;   // 16-byte chunks per thread
+  bf16x8 av[NU];
   if (EPI == EPI_POLY) {
     const bf16* auxb = g.aux + (long long)b * g.aux_bs + (long long)gi0 * g.aux_ld + gj0;
 #pragma unroll
-    for (int u = 0; u < 32; ++u) {
+    for (int u = 0; u < NU; ++u) {
       const int e = tid + GEMM_THREADS * u;
       av[u] = *(const bf16x8*)(auxb + (long long)(e >> 5) * g.aux_ld + (e & 31) * 8);
     }
@@ -280,13 +297,13 @@ void gemm_nt_bf16(GemmArgs g) {
   auto cswz = [](int i) { return ((i >> 3) & 3) | ((((i & 7) ^ (i >> 5)) & 7) << 2); };
   auto caddr = [&](int i, int j) { return i * 512 + 16 * ((j >> 3) ^ cswz(i)) + 2 * (j & 7); };
 #pragma unroll
-  for (int bi = 0; bi < 4; ++bi) {
-    const int il = 128 * wm + 32 * bi + r32;
+  for (int bi = 0; bi < BM; ++bi) {
+    const int il = WT_M * wm + 32 * bi + r32;
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
+    for (int bj = 0; bj < BN; ++bj) {
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        const int jl = 128 * wn + 32 * bj + 8 * gq + 4 * (lane >> 5);
+        const int jl = WT_N * wn + 32 * bj + 8 * gq + 4 * (lane >> 5);
         bf16x4 o;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -331,7 +348,7 @@ void gemm_nt_bf16(GemmArgs g) {
   const bool need_t = g.outT && (!g.sym || !diag);
   bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
 #pragma unroll
-  for (int u = 0; u < 32; ++u) {
+  for (int u = 0; u < NU; ++u) {
     const int e = tid + GEMM_THREADS * u;
     const int il = e >> 5, jc = (e & 31) * 8;
     char* lp = cs + il * 512 + 16 * ((jc >> 3) ^ cswz(il));
@@ -358,7 +375,7 @@ void gemm_nt_bf16(GemmArgs g) {
   if (!need_t) return;
   ring_barrier();
   bf16* outtb = g.outT + (long long)b * g.outT_bs;
-  for (int u = 0; u < 8; ++u) {
+  for (int u = 0; u < TILE * TILE / 32 / GEMM_THREADS; ++u) {
     const int e = tid + GEMM_THREADS * u;
     const int ic = (e & 31) * 8, jg = (e >> 5) * 4;   // rows ic..ic+7, columns jg..jg+3
     uint2 r[8];
