@@ -47,22 +47,25 @@ void set_error(const char* fmt, ...) {
 
 // ---------------------------------------------------------------------------
 // MFMA GEMM tile: 256 x 256 output per workgroup, 8 waves (two per SIMD) of
-// 128 x 64, K step 32, a 4-stage LDS ring (three K steps of loads in flight
-// while one is consumed).
+// 128 x 64, K stages of 64 in a 2-slot LDS ring (one stage of loads in flight
+// while the other is consumed), one workgroup barrier per stage.
 //
 // Operand tiles go global -> LDS with the gfx950 direct-to-LDS load
-// (global_load_lds_dwordx4: lane L of a wave writes 16 bytes at base + 16 L, no
-// VGPR round trip).  An LDS row is 32 bf16 = 64 B = 4 chunks of 16 B; chunk c of
-// row r sits in slot c ^ swz(r), swz(r) = (r >> 1) & 3, so the 16-byte fragment
-// reads of 8 consecutive rows hit distinct banks.  The swizzle is applied by
-// choosing, for each lane, which global chunk it fetches into its fixed LDS slot.
+// (buffer_load_dwordx4 ... lds: lane L of a wave writes 16 bytes at base + 16 L,
+// no VGPR round trip).  An LDS row is 64 bf16 = 128 B = 8 chunks of 16 B; chunk c
+// of row r sits in slot c ^ swz(r), so the 16-byte fragment reads hit distinct
+// banks.  The swizzle is applied by choosing, for each lane, which global chunk it
+// fetches into its fixed LDS slot.
 // ---------------------------------------------------------------------------
 constexpr int TILE = CHAIN_TILE;
-constexpr int TK = 32;
-constexpr int NSTAGE = 4;
+constexpr int TK = 64;
+constexpr int NSTAGE = 2;
+constexpr int KSUB = TK / 16;                // k16 MFMA substeps per stage
+constexpr int CHUNKS = TK / 8;               // 16-byte chunks per LDS row
 constexpr int ROWB = TK * 2;                 // bytes per LDS row
-constexpr int OPB = TILE * ROWB;             // bytes per operand tile (16 KB)
+constexpr int OPB = TILE * ROWB;             // bytes per operand tile (32 KB)
 constexpr int STAGEB = 2 * OPB;              // P + Q
+static_assert(KSUB == 4 && CHUNKS == 8, "the main loop is written for 64-wide K stages");
 // 8 waves, two per SIMD (so one wave's MFMAs fill the other's waits), as a
 // 2 x 4 grid of 128 x 64 wave tiles: 4 x 2 MFMA blocks of 32 x 32 per wave.
 constexpr int GEMM_WAVES = 8;
@@ -70,7 +73,8 @@ constexpr int GEMM_THREADS = 64 * GEMM_WAVES;
 constexpr int WAVES_N = 4;                      // waves along the Q rows (output columns)
 constexpr int WT_M = TILE / (GEMM_WAVES / WAVES_N), WT_N = TILE / WAVES_N;
 constexpr int BM = WT_M / 32, BN = WT_N / 32;   // MFMA blocks per wave
-constexpr int LQ = TILE / GEMM_WAVES / 16;      // loads per operand per stage per lane
+constexpr int LROWS = 64 / CHUNKS;                // tile rows per load instruction
+constexpr int LQ = TILE / GEMM_WAVES / LROWS;   // loads per operand per stage per lane
 constexpr int RING_BYTES = NSTAGE * STAGEB > 128 * 1024 ? NSTAGE * STAGEB : 128 * 1024;
 static_assert(RING_BYTES <= 160 * 1024, "LDS ring and epilogue tile must fit the 160 KB of a CU");
 // loads of the stages younger than the one waited for (8 per stage per wave)
@@ -110,7 +114,9 @@ __device__ __forceinline__ void decode_tile(const GemmArgs& g, int lid, int& b, 
   }
 }
 
-__device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
+// 16-byte slot of chunk c in LDS row r is c ^ lds_swz(r): the fragment reads of 8
+// consecutive rows (and of 16, on two 128-byte halves) hit distinct banks.
+__device__ __forceinline__ int lds_swz(int r) { return (r ^ (r >> 3)) & (CHUNKS - 1); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -145,21 +151,21 @@ void gemm_nt_bf16(GemmArgs g) {
   const bf16* Q = g.Q + (long long)b * g.q_bs + (long long)(tj * TILE) * g.q_ld;
 
   // Loader: buffer loads straight into LDS (buffer_load_dwordx4 ... lds).  Wave w,
-  // instruction q covers tile rows (TILE/GEMM_WAVES) w + 16q .. +15; lane L fills
-  // slot L & 3 of row (TILE/GEMM_WAVES) w + 16q + (L >> 2) with the global chunk
-  // slot ^ swz(row).  The per-lane byte
+  // instruction q covers tile rows (TILE/GEMM_WAVES) w + LROWS q .. +LROWS-1; lane L
+  // fills slot L % CHUNKS of row (TILE/GEMM_WAVES) w + LROWS q + L / CHUNKS with the
+  // global chunk slot ^ swz(row).  The per-lane byte
   // offsets are fixed for the whole K loop, the K step goes into the scalar offset
   // and the LDS destination (M0) is wave-uniform, so a load costs no VALU work.
   const __amdgpu_buffer_rsrc_t rP =
       __builtin_amdgcn_make_buffer_rsrc((void*)P, (short)0, TILE * g.p_ld * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t rQ =
       __builtin_amdgcn_make_buffer_rsrc((void*)Q, (short)0, TILE * g.q_ld * 2, 0x00020000);
-  const int lrow0 = (TILE / GEMM_WAVES) * wave + (lane >> 2);
-  const int lslot = lane & 3;
+  const int lrow0 = (TILE / GEMM_WAVES) * wave + lane / CHUNKS;
+  const int lslot = lane % CHUNKS;
   int boffP[LQ], boffQ[LQ];   // byte offsets within the tile
 #pragma unroll
   for (int q = 0; q < LQ; ++q) {
-    const int r = lrow0 + 16 * q;
+    const int r = lrow0 + LROWS * q;
     const int c = lslot ^ lds_swz(r);
     boffP[q] = (r * g.p_ld + c * 8) * 2;
     boffQ[q] = (r * g.q_ld + c * 8) * 2;
@@ -172,9 +178,9 @@ void gemm_nt_bf16(GemmArgs g) {
     char* dQ = dP + OPB;                                                               \
     const int so = (k0) * 2;                                                           \
     _Pragma("unroll") for (int q = 0; q < LQ; ++q) {                                   \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_ptr_t)(dP + q * 16 * ROWB), 16, \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_ptr_t)(dP + q * LROWS * ROWB), 16, \
                                                boffP[q], so, 0, 0);                    \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_ptr_t)(dQ + q * 16 * ROWB), 16, \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_ptr_t)(dQ + q * LROWS * ROWB), 16, \
                                                boffQ[q], so, 0, 0);                    \
     }                                                                                  \
   } while (0)
@@ -189,81 +195,94 @@ void gemm_nt_bf16(GemmArgs g) {
 
   const int r32 = lane & 31;
   const int hi = lane >> 5;
-  const int sw = lds_swz(r32);
-  // byte offsets of this lane's fragment rows (row 32i + r32 of the wave's half)
-  const int fP = (WT_M * wm + r32) * ROWB;
-  const int fQ = OPB + (WT_N * wn + r32) * ROWB;
-  const int fch0 = ((0 + hi) ^ sw) * 16, fch1 = ((2 + hi) ^ sw) * 16;
+  // byte offsets of this lane's fragments: row 32 i + r32 of the wave's P rows (and
+  // 32 j + r32 of its Q rows), 16-byte chunk 2 s + hi for k16 substep s
+  int offP[BM][KSUB], offQ[BN][KSUB];
+#pragma unroll
+  for (int i = 0; i < BM; ++i) {
+    const int row = WT_M * wm + 32 * i + r32;
+#pragma unroll
+    for (int st = 0; st < KSUB; ++st) offP[i][st] = row * ROWB + ((2 * st + hi) ^ lds_swz(row)) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < BN; ++j) {
+    const int row = WT_N * wn + 32 * j + r32;
+#pragma unroll
+    for (int st = 0; st < KSUB; ++st)
+      offQ[j][st] = OPB + row * ROWB + ((2 * st + hi) ^ lds_swz(row)) * 16;
+  }
 
   // Main loop, software-pipelined at two levels:
-  //  * LDS ring: stages kt+1..kt+NSTAGE-1 are in flight while stage kt is consumed.  The
-  //    prefetch is unconditional: past the last stage it re-fetches the last stage
-  //    into the free slot (never read), so every step waits on the same vmcnt and
-  //    the loop body is one basic block the scheduler can interleave.
-  //  * fragments: the k16 substep-0 fragments of stage kt+1 are read from LDS
-  //    under the substep-1 MFMAs of stage kt, and substep 1 under substep 0, so the
-  //    MFMA pipe never waits on LDS at the top of a step.
-  // The slot refilled at step kt (stage kt+NSTAGE-1) held stage kt-1, whose last fragment reads
-  // completed (lgkmcnt(0)) before the barrier of step kt-1.
+  //  * LDS ring: stages kt+1..kt+NSTAGE-1 are in flight while stage kt is consumed.
+  //    The prefetch is unconditional: past the last stage it re-fetches the last
+  //    stage into the free slot (never read), so every step waits on the same
+  //    vmcnt and the loop body has no branches.
+  //  * fragments: substep s+1 is read from LDS under the MFMAs of substep s, and
+  //    substep 0 of stage kt+1 under the last substep of stage kt, so the MFMA pipe
+  //    never waits on LDS; the one barrier per stage sits before the last substep.
+  // The slot refilled at step kt (stage kt+NSTAGE-1) held stage kt-1, whose last
+  // fragment reads completed (lgkmcnt(0)) before the barrier of step kt-1.
   const int nk = g.K / TK;
 #pragma unroll
   for (int p = 0; p < NSTAGE - 1; ++p) DMH_GLOAD(min(p, nk - 1) * TK, p);
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");   // stage 0 landed (own loads)
   ring_barrier();                                       // ... and everyone's
 
+#define DMH_RD(F, base, st)                                                            \
+  do {                                                                                 \
+    _Pragma("unroll") for (int i = 0; i < BM; ++i)                                     \
+      F##p[i] = *(const bf16x8*)((base) + offP[i][st]);                                \
+    _Pragma("unroll") for (int j = 0; j < BN; ++j)                                     \
+      F##q[j] = *(const bf16x8*)((base) + offQ[j][st]);                                \
+  } while (0)
+#define DMH_MM(F)                                                                      \
+  do {                                                                                 \
+    _Pragma("unroll") for (int i = 0; i < BM; ++i)                                     \
+      _Pragma("unroll") for (int j = 0; j < BN; ++j)                                   \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F##q[j], F##p[i], acc[i][j], 0, 0, 0); \
+  } while (0)
+  // MFMAs of one substep with the next substep's fragment reads among them
+#define DMH_SCHED_SUB()                                                                \
+  do {                                                                                 \
+    _Pragma("unroll") for (int x = 0; x < BM + BN; ++x) {                              \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                               \
+    }                                                                                  \
+    __builtin_amdgcn_sched_group_barrier(0x008, BM * BN - (BM + BN), 0);               \
+  } while (0)
+
   bf16x8 f0p[BM], f0q[BN], f1p[BM], f1q[BN];
-#pragma unroll
-  for (int i = 0; i < BM; ++i) f0p[i] = *(const bf16x8*)(smem + fP + i * 32 * ROWB + fch0);
-#pragma unroll
-  for (int j = 0; j < BN; ++j) f0q[j] = *(const bf16x8*)(smem + fQ + j * 32 * ROWB + fch0);
+  DMH_RD(f0, smem, 0);
   int s_cur = 0;   // ring slot of stage kt
   for (int kt = 0; kt < nk; ++kt) {
     const int s_nxt = s_cur + 1 == NSTAGE ? 0 : s_cur + 1;
     const int s_pre = s_cur == 0 ? NSTAGE - 1 : s_cur - 1;   // slot of stage kt + NSTAGE - 1
     const char* cur = smem + s_cur * STAGEB;
     const char* nxt = smem + s_nxt * STAGEB;
-#pragma unroll
-    for (int i = 0; i < BM; ++i) f1p[i] = *(const bf16x8*)(cur + fP + i * 32 * ROWB + fch1);
-#pragma unroll
-    for (int j = 0; j < BN; ++j) f1q[j] = *(const bf16x8*)(cur + fQ + j * 32 * ROWB + fch1);
     DMH_GLOAD(min(kt + NSTAGE - 1, nk - 1) * TK, s_pre);
-#pragma unroll
-    for (int i = 0; i < BM; ++i)
-#pragma unroll
-      for (int j = 0; j < BN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0q[j], f0p[i], acc[i][j], 0, 0, 0);
-    // interleave: substep-1 fragment reads, then the prefetch loads, among the MFMAs
-#pragma unroll
-    for (int x = 0; x < BM + BN; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    }
-#pragma unroll
-    for (int x = 0; x < 2 * LQ; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (direct-to-LDS prefetch)
-    }
+    DMH_RD(f1, cur, 1);
+    DMH_MM(f0);
+    DMH_RD(f0, cur, 2);
+    DMH_MM(f1);
+    DMH_RD(f1, cur, 3);
+    DMH_MM(f0);
+    // prefetch loads first, then substeps 0..2 with the reads of 1..3 among them
+    __builtin_amdgcn_sched_group_barrier(0x020, 2 * LQ, 0);   // VMEM (direct-to-LDS)
+    DMH_SCHED_SUB();
+    DMH_SCHED_SUB();
+    DMH_SCHED_SUB();
     // stage kt+1 landed: the younger loads in flight are those of stages
     // kt+2 .. kt+NSTAGE-1, and loads retire in issue order
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");
     ring_barrier();
-#pragma unroll
-    for (int i = 0; i < BM; ++i) f0p[i] = *(const bf16x8*)(nxt + fP + i * 32 * ROWB + fch0);
-#pragma unroll
-    for (int j = 0; j < BN; ++j) f0q[j] = *(const bf16x8*)(nxt + fQ + j * 32 * ROWB + fch0);
-#pragma unroll
-    for (int i = 0; i < BM; ++i)
-#pragma unroll
-      for (int j = 0; j < BN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1q[j], f1p[i], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int x = 0; x < BM + BN; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read (next substep-0 fragments)
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, BM * BN - (BM + BN), 0);
+    DMH_RD(f0, nxt, 0);
+    DMH_MM(f1);
+    DMH_SCHED_SUB();
     s_cur = s_nxt;
   }
+#undef DMH_RD
+#undef DMH_MM
+#undef DMH_SCHED_SUB
 #undef DMH_GLOAD
   // the re-fetches past the last stage may still be landing in LDS
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
