@@ -277,10 +277,12 @@ __global__ __launch_bounds__(64) void chol_inv(const double* __restrict__ part, 
 }
 
 // C (rows x RP) = Y (rows x RP) * M (RP x RP), per matrix; 64 rows per workgroup,
-// a 4 x 4 output block per thread.
+// a 4 x 4 output block per thread.  CT (optional): the same product transposed,
+// RP x ldct per matrix (the layout the skinny GEMMs read their small operand in).
 __global__ __launch_bounds__(256) void right_mult(const float* __restrict__ Y, int rows,
                                                   long long y_bs, const float* __restrict__ M,
-                                                  float* __restrict__ C, long long c_bs) {
+                                                  float* __restrict__ C, long long c_bs,
+                                                  float* __restrict__ CT, int ldct) {
   __shared__ __attribute__((aligned(16))) float Ms[RP * RP];
   __shared__ __attribute__((aligned(16))) float Ys[64][RP + 4];
   const int b = blockIdx.y, r0 = blockIdx.x * 64, tid = threadIdx.x;
@@ -318,6 +320,294 @@ __global__ __launch_bounds__(256) void right_mult(const float* __restrict__ Y, i
       *(float4*)&C[(long long)b * c_bs + (long long)row * RP + 4 * tx] =
           make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
   }
+  if (!CT) return;
+  float* CTb = CT + (long long)b * RP * ldct;
+  const int row0 = r0 + 4 * ty;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float* dst = CTb + (long long)(4 * tx + k) * ldct + row0;
+    if (row0 + 3 < rows && (ldct & 3) == 0) {
+      *(float4*)dst = make_float4(acc[0][k], acc[1][k], acc[2][k], acc[3][k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (row0 + i < rows) dst[i] = acc[i][k];
+    }
+  }
+}
+
+// dst (RP x ldd per matrix) = src^T for src (rows x cols, leading dim lds), zero
+// for the columns cols..RP-1: the transposed layout of the skinny GEMMs' small operand.
+__global__ __launch_bounds__(256) void transpose_rp(const float* __restrict__ src, int rows,
+                                                    int cols, int lds, long long s_bs,
+                                                    float* __restrict__ dst, int ldd) {
+  __shared__ float t[64][RP + 1];
+  const int b = blockIdx.y, r0 = blockIdx.x * 64, tid = threadIdx.x;
+  for (int e = tid; e < 64 * RP; e += 256) {
+    const int rr = e / RP, c = e % RP;
+    const int row = r0 + rr;
+    t[rr][c] = (row < rows && c < cols) ? src[(long long)b * s_bs + (long long)row * lds + c] : 0.f;
+  }
+  __syncthreads();
+  for (int e = tid; e < 64 * RP; e += 256) {
+    const int c = e / 64, rr = e % 64;
+    const int row = r0 + rr;
+    if (row < rows) dst[(long long)b * RP * ldd + (long long)c * ldd + row] = t[rr][c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny GEMMs on bf16 MFMA with split operands.  A stays fp32 in HBM; every fp32
+// value x is split on the fly into bf16 terms x = x_h + x_m + x_l (SPLITS = 3) or
+// x_h + x_l (SPLITS = 2) and the product is summed over the term pairs that matter
+// (6 of 9, resp. 3 of 4) in fp32 accumulators: SPLITS = 3 is accurate to fp32
+// rounding (all four products of the front-end use it: the Frobenius divisor is
+// formed from the Ritz values as ||A||^2 - sum lambda (2 - G), which amplifies
+// their error by the head-to-remainder energy ratio), SPLITS = 2 to ~2^-16 per
+// product.  No LDS: the A
+// operand goes from HBM straight into MFMA operand registers, so the kernels run
+// at the HBM roofline (4 B per element of A) instead of the fp32 MFMA rate.
+//
+// v_mfma_f32_32x32x16_bf16: lane l supplies row l%32, k = 8(l/32)..+7 of the first
+// operand and column l%32 of the second; the result D[8g + 4(l/32) + q][l%32] is
+// acc[4g + q].
+// ---------------------------------------------------------------------------
+template <int SPLITS>
+__device__ __forceinline__ void split_bf16(const float (&x)[8], bf16x8 (&t)[SPLITS]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float r = x[e];
+#pragma unroll
+    for (int s = 0; s < SPLITS; ++s) {
+      const bf16 h = f2bf(r);
+      t[s][e] = h;
+      r -= bf2f(h);
+    }
+  }
+}
+
+template <int SPLITS>
+__device__ __forceinline__ f32x16 mfma_split(const bf16x8 (&a)[SPLITS], const bf16x8 (&b)[SPLITS],
+                                             f32x16 acc) {
+  // smallest terms first
+  if (SPLITS == 3) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+  }
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+  return acc;
+}
+
+constexpr int SKR_ROWS = 256;   // rows of A per sk_rows workgroup (4 waves x 64)
+constexpr int SKC_COLS = 64;    // columns of A per sk_cols wave
+constexpr int SK_MAXS = 16;     // maximum row splits of sk_cols
+
+// C (n x RP, per matrix) = A (n x m) X, with X given transposed: XT (RP x ldxt),
+// XT[c][k] = X[k][c].  Needs m % 8 == 0.  asq: per-workgroup sums of squares of A.
+template <int SPLITS>
+__global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int n, int m,
+                                               const float* __restrict__ XT, int ldxt,
+                                               float* __restrict__ C, double* __restrict__ asq) {
+  const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hk = lane >> 5;
+  const int r0 = blockIdx.x * SKR_ROWS + wave * 64;
+  A += (long long)b * n * m;
+  XT += (long long)b * RP * ldxt;
+  C += (long long)b * n * RP;
+  const float* ap[2];
+  bool ain[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int i = r0 + 32 * rb + l32;
+    ain[rb] = i < n;
+    ap[rb] = A + (long long)(ain[rb] ? i : 0) * m + 8 * hk;
+  }
+  const float* xp[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) xp[cb] = XT + (long long)(32 * cb + l32) * ldxt + 8 * hk;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[rb][cb][e] = 0.f;
+  double sq = 0.0;
+  const int nk = (m + 15) / 16;
+  float4 an[2][2], xn[2][2];
+  auto load = [&](int ks, float4 (&a)[2][2], float4 (&x)[2][2]) {
+    const int k = 16 * ks;
+    const bool kin = k + 8 * hk < m;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const bool ok = kin && ain[rb];
+      a[rb][0] = ok ? *(const float4*)(ap[rb] + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      a[rb][1] = ok ? *(const float4*)(ap[rb] + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      x[cb][0] = kin ? *(const float4*)(xp[cb] + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      x[cb][1] = kin ? *(const float4*)(xp[cb] + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  load(0, an, xn);
+  for (int ks = 0; ks < nk; ++ks) {
+    float4 ac[2][2], xc[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) { ac[u][v] = an[u][v]; xc[u][v] = xn[u][v]; }
+    if (ks + 1 < nk) load(ks + 1, an, xn);
+    bf16x8 as[2][SPLITS], xs[2][SPLITS];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const float v[8] = {ac[rb][0].x, ac[rb][0].y, ac[rb][0].z, ac[rb][0].w,
+                          ac[rb][1].x, ac[rb][1].y, ac[rb][1].z, ac[rb][1].w};
+      if (asq) {
+        float f = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f = fmaf(v[e], v[e], f);
+        sq += (double)f;
+      }
+      split_bf16<SPLITS>(v, as[rb]);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const float v[8] = {xc[cb][0].x, xc[cb][0].y, xc[cb][0].z, xc[cb][0].w,
+                          xc[cb][1].x, xc[cb][1].y, xc[cb][1].z, xc[cb][1].w};
+      split_bf16<SPLITS>(v, xs[cb]);
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma_split<SPLITS>(xs[cb], as[rb], acc[rb][cb]);
+  }
+  // D[c][i] = C[i][c]: lane holds rows c = 32 cb + 8 g + 4 hk + q of column i = l32
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int i = r0 + 32 * rb + l32;
+    if (!ain[rb]) continue;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(float4*)&C[(long long)i * RP + 32 * cb + 8 * g + 4 * hk] =
+            make_float4(acc[rb][cb][4 * g], acc[rb][cb][4 * g + 1], acc[rb][cb][4 * g + 2],
+                        acc[rb][cb][4 * g + 3]);
+  }
+  if (asq) {
+    __shared__ double red[256];
+    red[tid] = sq;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+      if (tid < w) red[tid] += red[tid + w];
+      __syncthreads();
+    }
+    if (tid == 0) asq[(long long)b * gridDim.x + blockIdx.x] = red[0];
+  }
+}
+
+// Partial C = A^T Y over the rows [s * rps, (s+1) * rps) of split s = blockIdx.y:
+// part[s][b] (m x RP) = sum_i A[i][j] Y[i][c], with Y given transposed: YT (RP x
+// ldyt), YT[c][i] = Y[i][c].  One wave per 64 columns of A; lane l reads the
+// columns j0 + 2 l32 + {0, 1} of 8 consecutive rows, i.e. two 32-column MFMA
+// blocks (block e holds the columns j0 + 2 l32 + e).  Needs m % 2 == 0, n % 8 == 0.
+template <int SPLITS>
+__global__ __launch_bounds__(64) void sk_cols(const float* __restrict__ A, int n, int m,
+                                              const float* __restrict__ YT, int ldyt, int rps,
+                                              float* __restrict__ part) {
+  const int b = blockIdx.z, s = blockIdx.y, lane = threadIdx.x;
+  const int l32 = lane & 31, hk = lane >> 5;
+  const int nb = gridDim.z;
+  const int j0 = blockIdx.x * SKC_COLS;
+  const int jl = j0 + 2 * l32;           // this lane's two columns
+  const bool jin = jl < m;
+  A += (long long)b * n * m;
+  YT += (long long)b * RP * ldyt;
+  const int ib = s * rps, ie = min(n, ib + rps);
+  f32x16 acc[2][2];   // [e][cb]
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[e][cb][v] = 0.f;
+  const float* yp[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) yp[cb] = YT + (long long)(32 * cb + l32) * ldyt;
+  const int nk = (ie - ib + 15) / 16;
+  float2 an[8];
+  float4 yn[2][2];
+  auto load = [&](int ks, float2 (&a)[8], float4 (&y)[2][2]) {
+    const int i0 = ib + 16 * ks + 8 * hk;
+    const bool iin = i0 < ie;            // n % 8 == 0: 8-row chunks are whole
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      a[t] = (iin && jin) ? *(const float2*)(A + (long long)(i0 + t) * m + jl)
+                          : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      y[cb][0] = iin ? *(const float4*)(yp[cb] + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      y[cb][1] = iin ? *(const float4*)(yp[cb] + i0 + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  load(0, an, yn);
+  for (int ks = 0; ks < nk; ++ks) {
+    float2 ac[8];
+    float4 yc[2][2];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ac[t] = an[t];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) { yc[cb][0] = yn[cb][0]; yc[cb][1] = yn[cb][1]; }
+    if (ks + 1 < nk) load(ks + 1, an, yn);
+    bf16x8 as[2][SPLITS], ys[2][SPLITS];
+    {
+      const float v0[8] = {ac[0].x, ac[1].x, ac[2].x, ac[3].x, ac[4].x, ac[5].x, ac[6].x, ac[7].x};
+      const float v1[8] = {ac[0].y, ac[1].y, ac[2].y, ac[3].y, ac[4].y, ac[5].y, ac[6].y, ac[7].y};
+      split_bf16<SPLITS>(v0, as[0]);
+      split_bf16<SPLITS>(v1, as[1]);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const float v[8] = {yc[cb][0].x, yc[cb][0].y, yc[cb][0].z, yc[cb][0].w,
+                          yc[cb][1].x, yc[cb][1].y, yc[cb][1].z, yc[cb][1].w};
+      split_bf16<SPLITS>(v, ys[cb]);
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) acc[e][cb] = mfma_split<SPLITS>(ys[cb], as[e], acc[e][cb]);
+  }
+  // D[c][col] = C[j][c], col = l32 -> j = j0 + 2 l32 + e
+  float* pb = part + ((long long)s * nb + b) * m * RP;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int j = jl + e;
+    if (!jin) continue;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(float4*)&pb[(long long)j * RP + 32 * cb + 8 * g + 4 * hk] =
+            make_float4(acc[e][cb][4 * g], acc[e][cb][4 * g + 1], acc[e][cb][4 * g + 2],
+                        acc[e][cb][4 * g + 3]);
+  }
+}
+
+// C[b] = sum_s part[s][b] in split order (deterministic), float4 per thread
+__global__ __launch_bounds__(256) void sk_reduce(const float* __restrict__ part, int nsplit,
+                                                 long long per_split, float* __restrict__ C) {
+  const long long e4 = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e4 * 4 >= per_split) return;
+  float4 acc = *(const float4*)&part[e4 * 4];
+  for (int s = 1; s < nsplit; ++s) {
+    const float4 v = *(const float4*)&part[(long long)s * per_split + e4 * 4];
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  *(float4*)&C[e4 * 4] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -797,6 +1087,7 @@ __global__ __launch_bounds__(256) void copy_cols(const float* __restrict__ src, 
 // ---------------------------------------------------------------------------
 struct RsvdWs {
   float *Y, *Q, *Z, *Zq, *Bt, *U, *V, *M, *Ub, *UbS, *cw, *cr, *s;
+  float *XT, *QT, *part;   // split-bf16 skinny GEMMs: transposed small operands, row-split partials
   double *gram, *gramq, *asq;
   long long* k64;
   int *kint, *degen;
@@ -804,6 +1095,22 @@ struct RsvdWs {
 };
 
 static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// The split-bf16 skinny GEMMs need m and n to be multiples of 8; other shapes run the
+// fp32-MFMA kernels.
+static bool sk_fast(int n, int m) { return n % 8 == 0 && m % 8 == 0; }
+
+// Row splits of sk_cols: enough waves to fill the GPU (~4096), at least 256 rows each.
+static void sk_splits(int B, int n, int m, int* S, int* rps) {
+  const long long waves = (long long)ceil_div(m, SKC_COLS) * B;
+  int s = (int)((4096 + waves - 1) / waves);
+  s = s < 1 ? 1 : (s > SK_MAXS ? SK_MAXS : s);
+  while (s > 1 && n / s < 256) --s;
+  int r = ceil_div(n, s);
+  r = (r + 15) / 16 * 16;
+  *S = ceil_div(n, r);
+  *rps = r;
+}
 
 static RsvdWs rsvd_layout(void* base, int B, int n, int m) {
   RsvdWs w{};
@@ -831,6 +1138,13 @@ static RsvdWs rsvd_layout(void* base, int B, int n, int m) {
   w.k64 = (long long*)take((size_t)B * sizeof(long long));
   w.kint = (int*)take((size_t)B * sizeof(int));
   w.degen = (int*)take((size_t)B * sizeof(int));
+  if (sk_fast(n, m)) {
+    int S, rps;
+    sk_splits(B, n, m, &S, &rps);
+    w.XT = (float*)take((size_t)B * RP * m * sizeof(float));
+    w.QT = (float*)take((size_t)B * RP * n * sizeof(float));
+    w.part = (float*)take((size_t)S * B * m * RP * sizeof(float));
+  }
   w.bytes = off;
   return w;
 }
@@ -867,25 +1181,64 @@ static int gram(hipStream_t st, const float* Y, int B, int rows, double* part) {
   return DMH_OK;
 }
 
-// Q = orth(Y) by CholeskyQR (Y, Q: rows x RP), `passes` times.
+// Q = orth(Y) by CholeskyQR (Y, Q: rows x RP), `passes` times; QT (optional, RP x rows):
+// Q transposed, for the split-bf16 skinny GEMMs.
 static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int rows, int r,
-                int passes, const RsvdWs& w) {
+                int passes, const RsvdWs& w, float* QT = nullptr) {
   const float* src = Y;
   int rc;
   for (int p = 0; p < passes; ++p) {
-    float* dst = (p == passes - 1) ? Q : (p % 2 == 0 ? tmp : Q);
+    const bool last = p == passes - 1;
+    float* dst = last ? Q : (p % 2 == 0 ? tmp : Q);
     if ((rc = gram(st, src, B, rows, w.gram))) return rc;
     hipLaunchKernelGGL(chol_inv, dim3(B), dim3(64), 0, st, w.gram, r, w.M, w.degen);
     DMH_CHECK_LAUNCH("chol_inv");
     hipLaunchKernelGGL(right_mult, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, src, rows,
-                       (long long)rows * RP, w.M, dst, (long long)rows * RP);
+                       (long long)rows * RP, w.M, dst, (long long)rows * RP,
+                       last ? QT : (float*)nullptr, rows);
     DMH_CHECK_LAUNCH("right_mult");
     src = dst;
   }
   if (passes == 0) {
     hipMemcpyAsync(Q, Y, (size_t)B * rows * RP * sizeof(float), hipMemcpyDeviceToDevice, st);
     DMH_CHECK_LAUNCH("orth copy");
+    if (QT) {
+      hipLaunchKernelGGL(transpose_rp, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, Y, rows, RP,
+                         RP, (long long)rows * RP, QT, rows);
+      DMH_CHECK_LAUNCH("orth transpose");
+    }
   }
+  return DMH_OK;
+}
+
+// Y (n x RP) = A XT^T with the split-bf16 kernel (XT: RP x m); asq optional
+static int skr(hipStream_t st, int splits, const float* A, int B, int n, int m, const float* XT,
+               float* Y, double* asq) {
+  dim3 grid(ceil_div(n, SKR_ROWS), B);
+  if (splits == 3)
+    hipLaunchKernelGGL(sk_rows<3>, grid, dim3(256), 0, st, A, n, m, XT, m, Y, asq);
+  else
+    hipLaunchKernelGGL(sk_rows<2>, grid, dim3(256), 0, st, A, n, m, XT, m, Y, asq);
+  DMH_CHECK_LAUNCH("sk_rows");
+  return DMH_OK;
+}
+
+// C (m x RP) = A^T YT^T with the split-bf16 kernel (YT: RP x n), row splits reduced
+// in order
+static int skc(hipStream_t st, int splits, const float* A, int B, int n, int m, const float* YT,
+               float* C, const RsvdWs& w) {
+  int S, rps;
+  sk_splits(B, n, m, &S, &rps);
+  dim3 grid(ceil_div(m, SKC_COLS), S, B);
+  if (splits == 3)
+    hipLaunchKernelGGL(sk_cols<3>, grid, dim3(64), 0, st, A, n, m, YT, n, rps, w.part);
+  else
+    hipLaunchKernelGGL(sk_cols<2>, grid, dim3(64), 0, st, A, n, m, YT, n, rps, w.part);
+  DMH_CHECK_LAUNCH("sk_cols");
+  const long long per = (long long)B * m * RP;
+  hipLaunchKernelGGL(sk_reduce, dim3((unsigned)ceil_div(per / 4, 256)), dim3(256), 0, st, w.part,
+                     S, per, C);
+  DMH_CHECK_LAUNCH("sk_reduce");
   return DMH_OK;
 }
 
@@ -896,38 +1249,56 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
                      float* d, const RsvdWs& w) {
   int rc;
   hipMemsetAsync(w.degen, 0, (size_t)B * sizeof(int), st);
-  // Y = A Omega (and ||A||^2 partials) ; Q = orth(Y)
-  if ((rc = sg(st, SG_ROWSTREAM, A, B, n, m, Omega, r, r, (long long)m * r, w.Y,
-               (long long)n * RP, d ? w.asq : nullptr)))
-    return rc;
-  if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w))) return rc;
-  for (int it = 0; it < niter; ++it) {
-    // Z = orth(A^T Q) ; Q = orth(A Z)
-    if ((rc = sg(st, SG_COLSTREAM, A, B, n, m, w.Q, RP, RP, (long long)n * RP, w.Z,
-                 (long long)m * RP)))
-      return rc;
-    if ((rc = orth(st, w.Z, w.Zq, w.V, B, m, r, passes, w))) return rc;
-    if ((rc = sg(st, SG_ROWSTREAM, A, B, n, m, w.Zq, RP, RP, (long long)m * RP, w.Y,
-                 (long long)n * RP)))
+  const bool fast = sk_fast(n, m);
+  if (fast) {
+    // split-bf16 path, 3 terms (fp32-accurate) for every product
+    hipLaunchKernelGGL(transpose_rp, dim3(ceil_div(m, 64), B), dim3(256), 0, st, Omega, m, r, r,
+                       (long long)m * r, w.XT, m);
+    DMH_CHECK_LAUNCH("transpose Omega");
+    if ((rc = skr(st, 3, A, B, n, m, w.XT, w.Y, d ? w.asq : nullptr))) return rc;
+    if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT))) return rc;
+    for (int it = 0; it < niter; ++it) {
+      if ((rc = skc(st, 3, A, B, n, m, w.QT, w.Z, w))) return rc;
+      if ((rc = orth(st, w.Z, w.Zq, w.V, B, m, r, passes, w, w.XT))) return rc;
+      if ((rc = skr(st, 3, A, B, n, m, w.XT, w.Y, nullptr))) return rc;
+      if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT))) return rc;
+    }
+    if ((rc = skc(st, 3, A, B, n, m, w.QT, w.Bt, w))) return rc;
+  } else {
+    // Y = A Omega (and ||A||^2 partials) ; Q = orth(Y)
+    if ((rc = sg(st, SG_ROWSTREAM, A, B, n, m, Omega, r, r, (long long)m * r, w.Y,
+                 (long long)n * RP, d ? w.asq : nullptr)))
       return rc;
     if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w))) return rc;
+    for (int it = 0; it < niter; ++it) {
+      // Z = orth(A^T Q) ; Q = orth(A Z)
+      if ((rc = sg(st, SG_COLSTREAM, A, B, n, m, w.Q, RP, RP, (long long)n * RP, w.Z,
+                   (long long)m * RP)))
+        return rc;
+      if ((rc = orth(st, w.Z, w.Zq, w.V, B, m, r, passes, w))) return rc;
+      if ((rc = sg(st, SG_ROWSTREAM, A, B, n, m, w.Zq, RP, RP, (long long)m * RP, w.Y,
+                   (long long)n * RP)))
+        return rc;
+      if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w))) return rc;
+    }
+    // Bp^T = A^T Q (m x RP)
+    if ((rc = sg(st, SG_COLSTREAM, A, B, n, m, w.Q, RP, RP, (long long)n * RP, w.Bt,
+                 (long long)m * RP)))
+      return rc;
   }
-  // Bp^T = A^T Q (m x RP); H = Bp Bp^T = Gram of Bp^T
-  if ((rc = sg(st, SG_COLSTREAM, A, B, n, m, w.Q, RP, RP, (long long)n * RP, w.Bt,
-               (long long)m * RP)))
-    return rc;
+  // H = Bp Bp^T = Gram of Bp^T
   if ((rc = gram(st, w.Bt, B, m, w.gram))) return rc;
   if (d && (rc = gram(st, w.Q, B, n, w.gramq))) return rc;
   hipLaunchKernelGGL(eig_gate, dim3(B), dim3(EG_THREADS), 0, st, w.gram, gp, w.degen, w.s, RP, w.Ub,
                      w.UbS, k_out, w.kint, w.cw, w.cr, d ? w.gramq : nullptr,
-                     d ? w.asq : nullptr, ceil_div(n, SG_ROWS), d);
+                     d ? w.asq : nullptr, ceil_div(n, fast ? SKR_ROWS : SG_ROWS), d);
   DMH_CHECK_LAUNCH("eig_gate");
   // U = Q Ub ; V = Bp^T Ub diag(1/s)
   hipLaunchKernelGGL(right_mult, dim3(ceil_div(n, 64), B), dim3(256), 0, st, w.Q, n,
-                     (long long)n * RP, w.Ub, w.U, (long long)n * RP);
+                     (long long)n * RP, w.Ub, w.U, (long long)n * RP, (float*)nullptr, 0);
   DMH_CHECK_LAUNCH("right_mult (U)");
   hipLaunchKernelGGL(right_mult, dim3(ceil_div(m, 64), B), dim3(256), 0, st, w.Bt, m,
-                     (long long)m * RP, w.UbS, w.V, (long long)m * RP);
+                     (long long)m * RP, w.UbS, w.V, (long long)m * RP, (float*)nullptr, 0);
   DMH_CHECK_LAUNCH("right_mult (V)");
   return DMH_OK;
 }
@@ -1047,9 +1418,9 @@ int dmh_project(hipStream_t stream, const float* Q, const float* A, int batch, i
                      (const double*)nullptr, 0, (float*)nullptr);
   DMH_CHECK_LAUNCH("eig_gate");
   hipLaunchKernelGGL(right_mult, dim3(ceil_div(n, 64), batch), dim3(256), 0, stream, w.Q, n,
-                     (long long)n * RP, w.Ub, w.U, (long long)n * RP);
+                     (long long)n * RP, w.Ub, w.U, (long long)n * RP, (float*)nullptr, 0);
   hipLaunchKernelGGL(right_mult, dim3(ceil_div(m, 64), batch), dim3(256), 0, stream, w.Bt, m,
-                     (long long)m * RP, w.UbS, w.V, (long long)m * RP);
+                     (long long)m * RP, w.UbS, w.V, (long long)m * RP, (float*)nullptr, 0);
   DMH_CHECK_LAUNCH("right_mult (U, V)");
   return copy_usv(stream, w, batch, n, m, r, U, s, V);
 }

@@ -86,7 +86,12 @@ def test_clip_matches_reference_vectors(N, golden, key):
     X0, k, d = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
                             O.DIVISOR_PAD, 1, 1, None)
     assert k.cpu().tolist() == ref[f"{key}_k"].tolist()
-    np.testing.assert_allclose(d.cpu().numpy(), ref[f"{key}_d"], rtol=1e-5)
+    # d = ||A - U_k S_k V_k^T||_F + 1e-7 depends at first order on the rounding of the
+    # sketch products (single-pass fp32 CholeskyQR leaves Q^T Q - I ~ kappa*eps, and
+    # the head-to-remainder energy ratio, ~33 on clip2's first matrix, amplifies it):
+    # two correct fp32 implementations agree to the front-end tolerance, 1e-4.  The
+    # accuracy against the same algorithm in fp64 is held in test_config2_clip.
+    np.testing.assert_allclose(d.cpu().numpy(), ref[f"{key}_d"], rtol=SUBSPACE_TOL)
     assert rel(X0, torch.from_numpy(ref[f"{key}_X0f32"])) < SUBSPACE_TOL
     X0b, kb, _ = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
                               O.PE_PAD, 1, 1, torch.bfloat16)
