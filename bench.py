@@ -50,12 +50,21 @@ def ns_flops(groups, steps=5):
     return sum(B * steps * (4 * m * m * n + 2 * m ** 3) for B, n, m in groups)
 
 
-def make_inputs(groups, device, seed=1234):
+def make_inputs(groups, device, seed=1234, kind="spiked"):
+    """Synthetic momenta per group.  "gaussian": i.i.d. N(0, 1/n) entries (no QR, so
+    nothing from the solver library runs; the gate declines every matrix), for
+    hardware-counter runs whose NS-chain traffic does not depend on the values."""
+    import torch
     from defmuon_amd import synthetic as S
     out = []
     for gi, (B, n, m) in enumerate(groups):
-        out.append(S.spiked_batch(B, n, m, seed=seed + gi, n_spikes=8, hi=50.0, lo=10.0,
-                                  device=device))
+        if kind == "gaussian":
+            g = torch.Generator(device=device)
+            g.manual_seed(seed + gi)
+            out.append(torch.randn(B, n, m, device=device, generator=g) / math.sqrt(n))
+        else:
+            out.append(S.spiked_batch(B, n, m, seed=seed + gi, n_spikes=8, hi=50.0, lo=10.0,
+                                      device=device))
     return out
 
 
@@ -150,6 +159,13 @@ def main():
     ap.add_argument("--arm", default="deflated_ns_cut",
                     choices=["deflated_ns_cut", "deflated_pe_cut"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--inputs", default="spiked", choices=["spiked", "gaussian"],
+                    help="synthetic momenta: spiked spectra (default) or i.i.d. Gaussian "
+                         "(for counter runs; no solver call)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="before the steps, copy a MIB-MiB fp32 buffer three times with "
+                         "torch's copy kernel: a known-size reference for HBM byte "
+                         "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the polar path "
@@ -168,8 +184,16 @@ def main():
     dev = torch.device("cuda", 0)
     groups = WORKLOADS[args.workload]
     fac = C.ARMS[args.arm]()
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration * 2 ** 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: copy calibration: 3 x {args.copy_calibration} MiB read + written")
+        del src, dst
     log(f"bench: generating inputs for {args.workload}: {groups}")
-    stacks = make_inputs(groups, dev)
+    stacks = make_inputs(groups, dev, kind=args.inputs)
     torch.cuda.synchronize()
 
     log(f"bench: warmup {args.warmup}")
@@ -205,6 +229,12 @@ def main():
         cpu = cpu_baseline(groups, args.arm)
 
     nmat = sum(B for B, _, _ in groups)
+    # HBM traffic of the NS chain from the committed counter runs (same workload and arm)
+    traffic = {}
+    tpath = os.path.join(ROOT, "profiles", "ns_chain_traffic.json")
+    if args.workload == "gpt2-large" and args.arm == "deflated_ns_cut" and os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f)
     out = {
         "metric": "polar steps/sec (GPT-2-large all matrices, 1 GPU) + % bf16 MFMA peak",
         "value": 1e3 / ms_per_step,
@@ -223,7 +253,13 @@ def main():
                                + " + ".join(f"{B}x({n},{m})" for B, n, m in groups),
                    "matrices": nmat, "ns_steps": 5, "arm": args.arm},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
+                     "traffic": traffic.get("ns_chain_hbm_bytes_per_step"),
+                     "traffic_scope": ("HBM bytes per polar step over the NS chain launches, "
+                                       "measured with rocprofv3 --pmc FETCH_SIZE (x2) and "
+                                       "WRITE_SIZE (x1), scales from torch's copy kernel; "
+                                       + traffic.get("source", "not measured"))
+                     if traffic else None,
                      "kernel": "NS chain (gemm_nt_bf16 K1/K2/K3 launches of a polar step), "
                                "canonical dense 4m^2n+2m^3 FLOP per matrix-iteration",
                      "flops_per_step": flops, "ns_ms_per_step": ns_ms},
