@@ -12,10 +12,10 @@ struct ChainDims {
   int n, m, np, mp;   // tall operand T is n x m; padded to multiples of CHAIN_TILE
 };
 
-// Workspace of one chain call: T/W (iterate, both orientations) double-buffered,
-// A = W W^T and B = bA + cA^2, and the entry's norm partials.
+// Workspace of one chain call: the tall iterate T double-buffered, A = T^T T and
+// B = bA + cA^2 + aI, and the entry's norm partials.
 struct ChainWs {
-  bf16 *T0, *W0, *T1, *W1, *A, *B;
+  bf16 *T0, *T1, *A, *B;
   double* partials;
   size_t bytes;
 };
@@ -23,7 +23,7 @@ struct ChainWs {
 ChainDims chain_dims(int rows, int cols, int orient_tall);
 ChainWs chain_ws(void* ws, int batch, const ChainDims& d);   // ws == nullptr: sizes only
 
-// Run `steps` iterations from T0/W0 already packed in the workspace; the result
+// Run `steps` iterations from T0 already packed in the workspace; the result
 // goes to `out` (batch, rows, cols) bf16 in the orientation given.
 int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const ChainDims& d,
                      int orient_tall, const double* coeffs, int steps, bf16* out);

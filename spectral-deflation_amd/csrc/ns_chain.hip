@@ -6,19 +6,21 @@
 //   _horner_iterate               defmuon/optim/deflation_batched.py:196-211
 // for a batch of same-shape matrices in one launch per GEMM phase.
 //
-// Layout.  Every matrix of the batch is held twice in a zero-padded workspace,
-// as W (m x n, the wide convention, m <= n) and as T = W^T (n x m), both bf16
-// row-major with m, n rounded up to the 256 tile.  One iteration (a, b, c) is
+// Layout.  Every matrix of the batch is held as the tall iterate T (n x m, n >= m;
+// W = T^T is the wide convention), bf16 row-major in a zero-padded workspace with
+// m, n rounded up to the 256 tile.  One iteration (a, b, c) is
 //
-//   K1  A  = W W^T                  (m x m, K = n)  symmetric: upper tiles only
+//   K1  A  = T^T T                  (m x m, K = n)  symmetric: upper tiles only
 //   K2  B' = b A + c A A + a I      (m x m, K = m)  symmetric: upper tiles only
-//   K3  T' = T B' ; W' = T'^T       (n x m, K = m)
+//   K3  T' = T B'                   (n x m, K = m)
 //
-// so every product is an "NT" GEMM C[i][j] = sum_k P[i][k] Q[j][k] whose two
-// operands are both K-contiguous, which is the layout the MFMA operand
-// registers want (A and B' symmetric make A A and T B' NT products).  Zero
-// padding is a fixed point of every phase (a I is added on the m true diagonal
-// entries only), so no kernel needs bounds checks on its loads.
+// K2 and K3 are "NT" GEMMs C[i][j] = sum_k P[i][k] Q[j][k] whose two operands are
+// K-contiguous rows (A and B' are symmetric), the layout the MFMA operand
+// registers want.  K1 contracts over the rows of T: its operand tiles are loaded
+// K-major and turned into MFMA fragments by the transposing LDS read of gfx950,
+// so the iterate is never stored transposed.  Zero padding is a fixed point of
+// every phase (a I is added on the m true diagonal entries only), so no kernel
+// needs bounds checks on its loads.
 //
 // Rounding.  A is stored bf16; B' = bf16(b*A + bf16(c*AA) + a*I); T' = bf16(T B')
 // with fp32 accumulation.  The reference's compiled graph rounds c*A to bf16
@@ -46,9 +48,17 @@ void set_error(const char* fmt, ...) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA GEMM tile: 256 x 256 output per workgroup, 8 waves (two per SIMD) of
-// 128 x 64, K stages of 64 in a 2-slot LDS ring (one stage of loads in flight
-// while the other is consumed), one workgroup barrier per stage.
+// MFMA GEMM: persistent workgroups (one per CU) over 256 x 256 output tiles, 8
+// waves (two per SIMD) of 128 x 64, K stages of 64 in a 2-slot LDS ring (one
+// stage of loads in flight while the other is consumed), one workgroup barrier
+// per stage.
+//
+// Each workgroup walks a list of tiles.  While the MFMAs of a tile's last K stage
+// run, the first stage of the workgroup's next tile is already loading into the
+// free ring slot, and the epilogue goes through a small per-wave staging area
+// outside the ring, so it needs no workgroup barrier and overlaps those loads;
+// workgroup start-up and the first-stage load latency are paid once per CU, not
+// once per tile.
 //
 // Operand tiles go global -> LDS with the gfx950 direct-to-LDS load
 // (buffer_load_dwordx4 ... lds: lane L of a wave writes 16 bytes at base + 16 L,
@@ -75,19 +85,24 @@ constexpr int WT_M = TILE / (GEMM_WAVES / WAVES_N), WT_N = TILE / WAVES_N;
 constexpr int BM = WT_M / 32, BN = WT_N / 32;   // MFMA blocks per wave
 constexpr int LROWS = 64 / CHUNKS;                // tile rows per load instruction
 constexpr int LQ = TILE / GEMM_WAVES / LROWS;   // loads per operand per stage per lane
-constexpr int RING_BYTES = NSTAGE * STAGEB > 128 * 1024 ? NSTAGE * STAGEB : 128 * 1024;
-static_assert(RING_BYTES <= 160 * 1024, "LDS ring and epilogue tile must fit the 160 KB of a CU");
-// loads of the stages younger than the one waited for (8 per stage per wave)
-constexpr int RING_VMCNT = 2 * LQ * (NSTAGE - 2);
+static_assert(NSTAGE == 2, "the ring waits are written for two slots (vmcnt(0))");
+constexpr int RING_BYTES = NSTAGE * STAGEB;
+// epilogue staging: one 32 x 64 bf16 block row of the wave's output at a time
+constexpr int EPI_WAVE_BYTES = 32 * WT_N * 2;
+static_assert(WT_N == 64, "the epilogue staging is written for 64-column wave tiles");
+constexpr int SMEM_BYTES = RING_BYTES + GEMM_WAVES * EPI_WAVE_BYTES;
+static_assert(SMEM_BYTES <= 160 * 1024, "LDS ring and epilogue staging must fit the 160 KB of a CU");
 
 enum { EPI_STORE = 0, EPI_POLY = 1 };
 
 struct GemmArgs {
   const bf16* P; long long p_bs; int p_ld;      // rows i of C
   const bf16* Q; long long q_bs; int q_ld;      // rows j of C
-  int K;                                         // multiple of TK
+  int K;                                         // multiple of TK, <= p_ld and q_ld
   int tiles_m, tiles_n;                          // tiles per matrix
   int sym;                                       // upper-triangular tiles, mirrored stores
+  int total_tiles;                               // over the batch
+  int batch, rev;                                // rev: walk the batch from its last matrix
   float alpha, beta;                             // POLY: (b, c)
   float diag_add; int diag_lim;                  // POLY: + diag_add on C[i][i], i < diag_lim
   const bf16* aux; long long aux_bs; int aux_ld; // POLY: A (indexed [i][j])
@@ -112,6 +127,25 @@ __device__ __forceinline__ void decode_tile(const GemmArgs& g, int lid, int& b, 
     ti = t / g.tiles_n;
     tj = t - ti * g.tiles_n;
   }
+  if (g.rev) b = g.batch - 1 - b;
+}
+
+// Tiles of this workgroup: first, first + step, ... < end.  The dispatcher deals
+// workgroups round-robin over the 8 XCDs, so workgroup w runs on XCD w % 8; the
+// tile list is cut into 8 contiguous ranges, one per XCD, sized by the XCD's
+// number of workgroups, and the workgroups of an XCD take its range round-robin.
+// At any moment the CUs of one XCD work on consecutive tiles, whose operands
+// share that XCD's L2.
+__device__ __forceinline__ void tile_range(int total, int& first, int& step, int& end) {
+  constexpr int NXCD = 8;
+  const int G = gridDim.x, bid = blockIdx.x;
+  const int x = bid % NXCD, s = bid / NXCD;
+  const int q = G / NXCD, r = G % NXCD;
+  const int cnt = q + (x < r ? 1 : 0);
+  const int pre = x * q + (x < r ? x : r);
+  first = (int)((long long)total * pre / G) + s;
+  step = cnt;
+  end = (int)((long long)total * (pre + cnt) / G);
 }
 
 // 16-byte slot of chunk c in LDS row r is c ^ lds_swz(r): the fragment reads of 8
@@ -124,7 +158,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // its own direct-to-LDS loads of the stage about to be read, and its fragment
 // reads of the stage about to be refilled have been consumed by its MFMAs, so the
 // barrier needs no memory fence: __syncthreads() would make the compiler drain
-// all outstanding loads (vmcnt(0)), i.e. the whole prefetch ring, at every step.
+// all outstanding loads (vmcnt(0)) at every step.
 // The empty asm statements keep the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void ring_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -132,108 +166,151 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int EPI>
+// Buffer descriptor of one operand tile.  Row-operand layout (TNL = 0): rows t*TILE..
+// +TILE-1 of a K-contiguous matrix.  K-major layout (TNL = 1): columns t*TILE..+TILE-1
+// of a matrix whose row k holds the operand's values for contraction index k.
+template <int TNL>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16* base, long long bs,
+                                                           int ld, int K, int b, int t) {
+  if (TNL) {
+    const bf16* p = base + (long long)b * bs + (long long)t * TILE;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, K * ld * 2, 0x00020000);
+  }
+  const bf16* p = base + (long long)b * bs + (long long)(t * TILE) * ld;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, TILE * ld * 2, 0x00020000);
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
+
+// MFMA operand fragment (8 consecutive k of one column) from a K-major LDS tile,
+// with the gfx950 transposing LDS read (ds_read_b64_tr_b16): within each group of
+// 16 lanes, result lane j, element e is element j % 4 of the 8-byte chunk addressed
+// by lane 4 e + j / 4.  Lane 16 g + 4 e + q addresses row k0 + e, columns c0 + 4 q
+// .. +3, so lane 16 g + j receives column c0 + j at rows k0 .. k0+3; the second read
+// (rows k0+4 .. k0+7) is 4 rows = 2048 bytes further.
+__device__ __forceinline__ bf16x8 lds_tr_frag(const char* p) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(p));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(p + 4 * 512));
+  const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), h4 = __builtin_bit_cast(bf16x4, hi);
+  return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Store 8 consecutive bf16 at dst (elements q with mask bit q set); a full, aligned
+// chunk leaves as one 16-byte store.
+__device__ __forceinline__ void store8(bf16* dst, const bf16x8& v, unsigned mask, bool aligned) {
+  if (mask == 0xffu && aligned) {
+    *(bf16x8*)dst = v;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (mask & (1u << q)) dst[q] = v[q];
+  }
+}
+
+// TNL = 0: C[i][j] = sum_k P[i][k] Q[j][k] (both operands K-contiguous rows).
+// TNL = 1: C[i][j] = sum_k P[k][i] Q[k][j] (both operands K-major: their row k holds
+//          the values of every output index for contraction index k).
+template <int EPI, int TNL>
 __global__ __attribute__((amdgpu_flat_work_group_size(GEMM_THREADS, GEMM_THREADS),
                           amdgpu_waves_per_eu(GEMM_WAVES / 4, GEMM_WAVES / 4)))
 void gemm_nt_bf16(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[RING_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
 
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  int b, ti, tj;
-  decode_tile(g, lid, b, ti, tj);
+  int lid, lstep, lend;
+  tile_range(g.total_tiles, lid, lstep, lend);
+  if (lid >= lend) return;   // uniform over the workgroup
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-  const bf16* P = g.P + (long long)b * g.p_bs + (long long)(ti * TILE) * g.p_ld;
-  const bf16* Q = g.Q + (long long)b * g.q_bs + (long long)(tj * TILE) * g.q_ld;
-
   // Loader: buffer loads straight into LDS (buffer_load_dwordx4 ... lds).  Wave w,
   // instruction q covers tile rows (TILE/GEMM_WAVES) w + LROWS q .. +LROWS-1; lane L
   // fills slot L % CHUNKS of row (TILE/GEMM_WAVES) w + LROWS q + L / CHUNKS with the
-  // global chunk slot ^ swz(row).  The per-lane byte
-  // offsets are fixed for the whole K loop, the K step goes into the scalar offset
-  // and the LDS destination (M0) is wave-uniform, so a load costs no VALU work.
-  const __amdgpu_buffer_rsrc_t rP =
-      __builtin_amdgcn_make_buffer_rsrc((void*)P, (short)0, TILE * g.p_ld * 2, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rQ =
-      __builtin_amdgcn_make_buffer_rsrc((void*)Q, (short)0, TILE * g.q_ld * 2, 0x00020000);
-  const int lrow0 = (TILE / GEMM_WAVES) * wave + lane / CHUNKS;
-  const int lslot = lane % CHUNKS;
+  // global chunk slot ^ swz(row).  The per-lane byte offsets are the same for every
+  // tile and K step (the tile base is in the buffer descriptor, the K step in the
+  // scalar offset) and the LDS destination (M0) is wave-uniform, so a load costs no
+  // VALU work.
+  //
+  // K-major tiles (TNL) are 64 rows (k) of 512 B (32 chunks of 16 B, the 256 output
+  // indices); chunk c of row r sits in slot c ^ 4 (r & 3), which spreads the
+  // transposing fragment reads (4 rows x 4 chunks per 16 lanes) over every bank.
+  // Instruction q of wave w fills rows 8 w + 2 q and 8 w + 2 q + 1 (1 KB), so the
+  // LDS destinations are the same as for the row-operand tiles.
   int boffP[LQ], boffQ[LQ];   // byte offsets within the tile
+  if (TNL) {
+    static_assert(TK / GEMM_WAVES == 2 * LQ && TILE * 2 == 32 * 16, "K-major loader layout");
 #pragma unroll
-  for (int q = 0; q < LQ; ++q) {
-    const int r = lrow0 + LROWS * q;
-    const int c = lslot ^ lds_swz(r);
-    boffP[q] = (r * g.p_ld + c * 8) * 2;
-    boffQ[q] = (r * g.q_ld + c * 8) * 2;
+    for (int q = 0; q < LQ; ++q) {
+      const int r = (TK / GEMM_WAVES) * wave + 2 * q + (lane >> 5);
+      const int c = (lane & 31) ^ (4 * (r & 3));
+      boffP[q] = (r * g.p_ld + c * 8) * 2;
+      boffQ[q] = (r * g.q_ld + c * 8) * 2;
+    }
+  } else {
+    const int lrow0 = (TILE / GEMM_WAVES) * wave + lane / CHUNKS;
+    const int lslot = lane % CHUNKS;
+#pragma unroll
+    for (int q = 0; q < LQ; ++q) {
+      const int r = lrow0 + LROWS * q;
+      const int c = lslot ^ lds_swz(r);
+      boffP[q] = (r * g.p_ld + c * 8) * 2;
+      boffQ[q] = (r * g.q_ld + c * 8) * 2;
+    }
   }
+  // scalar byte offset of K stage k0: along the row, or down k0 rows (K-major)
+  const int kstepP = TNL ? g.p_ld * 2 : 2, kstepQ = TNL ? g.q_ld * 2 : 2;
   char* const lds_wave = smem + wave * (TILE / GEMM_WAVES) * ROWB;   // this wave's first row
 
-#define DMH_GLOAD(k0, st)                                                              \
+#define DMH_GLOAD(rp, rq, k0, st)                                                      \
   do {                                                                                 \
     char* dP = lds_wave + (st) * STAGEB;                                               \
     char* dQ = dP + OPB;                                                               \
-    const int so = (k0) * 2;                                                           \
+    const int soP = (k0) * kstepP, soQ = (k0) * kstepQ;                                \
     _Pragma("unroll") for (int q = 0; q < LQ; ++q) {                                   \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rP, (lds_ptr_t)(dP + q * LROWS * ROWB), 16, \
-                                               boffP[q], so, 0, 0);                    \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rQ, (lds_ptr_t)(dQ + q * LROWS * ROWB), 16, \
-                                               boffQ[q], so, 0, 0);                    \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_ptr_t)(dP + q * LROWS * ROWB), 16, \
+                                               boffP[q], soP, 0, 0);                   \
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr_t)(dQ + q * LROWS * ROWB), 16, \
+                                               boffQ[q], soQ, 0, 0);                   \
     }                                                                                  \
   } while (0)
-
-  f32x16 acc[BM][BN];
-#pragma unroll
-  for (int i = 0; i < BM; ++i)
-#pragma unroll
-    for (int j = 0; j < BN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int r32 = lane & 31;
   const int hi = lane >> 5;
   // byte offsets of this lane's fragments: row 32 i + r32 of the wave's P rows (and
   // 32 j + r32 of its Q rows), 16-byte chunk 2 s + hi for k16 substep s
+  // (K-major tiles: first of the two transposing reads of column block c0, rows
+  // 16 st + 8 (g >> 1) + e, with g = lane / 16, e = (lane / 4) % 4, q = lane % 4)
   int offP[BM][KSUB], offQ[BN][KSUB];
+  auto frag_off = [&](int c0, int st) {
+    if (TNL) {
+      const int gq = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+      const int k = 16 * st + 8 * (gq >> 1) + e;
+      const int c = c0 + 16 * (gq & 1) + 4 * q;
+      return k * 512 + (((c >> 3) ^ (4 * (k & 3))) * 16) + (c & 7) * 2;
+    }
+    const int row = c0 + r32;
+    return row * ROWB + ((2 * st + hi) ^ lds_swz(row)) * 16;
+  };
 #pragma unroll
-  for (int i = 0; i < BM; ++i) {
-    const int row = WT_M * wm + 32 * i + r32;
+  for (int i = 0; i < BM; ++i)
 #pragma unroll
-    for (int st = 0; st < KSUB; ++st) offP[i][st] = row * ROWB + ((2 * st + hi) ^ lds_swz(row)) * 16;
-  }
+    for (int st = 0; st < KSUB; ++st) offP[i][st] = frag_off(WT_M * wm + 32 * i, st);
 #pragma unroll
-  for (int j = 0; j < BN; ++j) {
-    const int row = WT_N * wn + 32 * j + r32;
+  for (int j = 0; j < BN; ++j)
 #pragma unroll
-    for (int st = 0; st < KSUB; ++st)
-      offQ[j][st] = OPB + row * ROWB + ((2 * st + hi) ^ lds_swz(row)) * 16;
-  }
-
-  // Main loop, software-pipelined at two levels:
-  //  * LDS ring: stages kt+1..kt+NSTAGE-1 are in flight while stage kt is consumed.
-  //    The prefetch is unconditional: past the last stage it re-fetches the last
-  //    stage into the free slot (never read), so every step waits on the same
-  //    vmcnt and the loop body has no branches.
-  //  * fragments: substep s+1 is read from LDS under the MFMAs of substep s, and
-  //    substep 0 of stage kt+1 under the last substep of stage kt, so the MFMA pipe
-  //    never waits on LDS; the one barrier per stage sits before the last substep.
-  // The slot refilled at step kt (stage kt+NSTAGE-1) held stage kt-1, whose last
-  // fragment reads completed (lgkmcnt(0)) before the barrier of step kt-1.
-  const int nk = g.K / TK;
-#pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p) DMH_GLOAD(min(p, nk - 1) * TK, p);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");   // stage 0 landed (own loads)
-  ring_barrier();                                       // ... and everyone's
+    for (int st = 0; st < KSUB; ++st) offQ[j][st] = OPB + frag_off(WT_N * wn + 32 * j, st);
 
 #define DMH_RD(F, base, st)                                                            \
   do {                                                                                 \
     _Pragma("unroll") for (int i = 0; i < BM; ++i)                                     \
-      F##p[i] = *(const bf16x8*)((base) + offP[i][st]);                                \
+      F##p[i] = TNL ? lds_tr_frag((base) + offP[i][st])                                \
+                    : *(const bf16x8*)((base) + offP[i][st]);                          \
     _Pragma("unroll") for (int j = 0; j < BN; ++j)                                     \
-      F##q[j] = *(const bf16x8*)((base) + offQ[j][st]);                                \
+      F##q[j] = TNL ? lds_tr_frag((base) + offQ[j][st])                                \
+                    : *(const bf16x8*)((base) + offQ[j][st]);                          \
   } while (0)
 #define DMH_MM(F)                                                                      \
   do {                                                                                 \
@@ -246,191 +323,224 @@ void gemm_nt_bf16(GemmArgs g) {
   do {                                                                                 \
     _Pragma("unroll") for (int x = 0; x < BM + BN; ++x) {                              \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               \
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                               \
+      __builtin_amdgcn_sched_group_barrier(0x100, TNL ? 2 : 1, 0);                     \
     }                                                                                  \
     __builtin_amdgcn_sched_group_barrier(0x008, BM * BN - (BM + BN), 0);               \
   } while (0)
 
+  const int nk = g.K / TK;
+  int b, ti, tj;
+  decode_tile(g, lid, b, ti, tj);
+  __amdgpu_buffer_rsrc_t rP = tile_rsrc<TNL>(g.P, g.p_bs, g.p_ld, g.K, b, ti);
+  __amdgpu_buffer_rsrc_t rQ = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_ld, g.K, b, tj);
+  DMH_GLOAD(rP, rQ, 0, 0);
+
+  char* const stg = smem + RING_BYTES + wave * EPI_WAVE_BYTES;   // this wave's staging
+  f32x16 acc[BM][BN];
   bf16x8 f0p[BM], f0q[BN], f1p[BM], f1q[BN];
-  DMH_RD(f0, smem, 0);
-  int s_cur = 0;   // ring slot of stage kt
-  for (int kt = 0; kt < nk; ++kt) {
-    const int s_nxt = s_cur + 1 == NSTAGE ? 0 : s_cur + 1;
-    const int s_pre = s_cur == 0 ? NSTAGE - 1 : s_cur - 1;   // slot of stage kt + NSTAGE - 1
-    const char* cur = smem + s_cur * STAGEB;
-    const char* nxt = smem + s_nxt * STAGEB;
-    DMH_GLOAD(min(kt + NSTAGE - 1, nk - 1) * TK, s_pre);
-    DMH_RD(f1, cur, 1);
-    DMH_MM(f0);
-    DMH_RD(f0, cur, 2);
-    DMH_MM(f1);
-    DMH_RD(f1, cur, 3);
-    DMH_MM(f0);
-    // prefetch loads first, then substeps 0..2 with the reads of 1..3 among them
-    __builtin_amdgcn_sched_group_barrier(0x020, 2 * LQ, 0);   // VMEM (direct-to-LDS)
-    DMH_SCHED_SUB();
-    DMH_SCHED_SUB();
-    DMH_SCHED_SUB();
-    // stage kt+1 landed: the younger loads in flight are those of stages
-    // kt+2 .. kt+NSTAGE-1, and loads retire in issue order
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(RING_VMCNT) : "memory");
+  int s_cur = 0;   // ring slot of the stage being consumed
+  for (;;) {
+    // the workgroup's next tile, if any (its first stages are loaded and prefetched
+    // during this tile's last steps)
+    const int nlid = lid + lstep;
+    const bool more = nlid < lend;
+    int nb = b, nti = ti, ntj = tj;
+    if (more) decode_tile(g, nlid, nb, nti, ntj);
+    const __amdgpu_buffer_rsrc_t rPn = tile_rsrc<TNL>(g.P, g.p_bs, g.p_ld, g.K, nb, nti);
+    const __amdgpu_buffer_rsrc_t rQn = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_ld, g.K, nb, ntj);
+
+    // Main loop of one tile, software-pipelined at two levels:
+    //  * LDS ring: stage kt+1 is in flight while stage kt is consumed;
+    //  * fragments: substep s+1 is read from LDS under the MFMAs of substep s, and
+    //    substep 0 of stage kt+1 under the last substep of stage kt, so the MFMA pipe
+    //    never waits on LDS; the one barrier per stage sits before the last substep.
+    // The slot refilled at step kt (stage kt+1) held stage kt-1, whose last fragment
+    // reads completed (lgkmcnt(0)) before the barrier of step kt-1.  The wait for
+    // stage 0 also covers the previous tile's epilogue stores (vmcnt counts both).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     ring_barrier();
-    DMH_RD(f0, nxt, 0);
-    DMH_MM(f1);
-    DMH_SCHED_SUB();
-    s_cur = s_nxt;
+#pragma unroll
+    for (int i = 0; i < BM; ++i)
+#pragma unroll
+      for (int j = 0; j < BN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    DMH_RD(f0, smem + s_cur * STAGEB, 0);
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      const int s_nxt = s_cur ^ 1;
+      const char* cur = smem + s_cur * STAGEB;
+      const char* nxt = smem + s_nxt * STAGEB;
+      DMH_GLOAD(rP, rQ, (kt + 1) * TK, s_nxt);
+      DMH_RD(f1, cur, 1);
+      DMH_MM(f0);
+      DMH_RD(f0, cur, 2);
+      DMH_MM(f1);
+      DMH_RD(f1, cur, 3);
+      DMH_MM(f0);
+      // prefetch loads first, then substeps 0..2 with the reads of 1..3 among them
+      __builtin_amdgcn_sched_group_barrier(0x020, 2 * LQ, 0);   // VMEM (direct-to-LDS)
+      DMH_SCHED_SUB();
+      DMH_SCHED_SUB();
+      DMH_SCHED_SUB();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");        // stage kt+1 landed (own loads)
+      ring_barrier();                                          // ... and everyone's
+      DMH_RD(f0, nxt, 0);
+      DMH_MM(f1);
+      DMH_SCHED_SUB();
+      s_cur = s_nxt;
+    }
+    // Last stage: the next tile's first stage goes into the free slot (it held stage
+    // nk-2, or the previous tile's last stage, both consumed before a barrier) and
+    // stays in flight under the epilogue.
+    if (more) DMH_GLOAD(rPn, rQn, 0, s_cur ^ 1);
+    {
+      const char* cur = smem + s_cur * STAGEB;
+      DMH_RD(f1, cur, 1);
+      DMH_MM(f0);
+      DMH_RD(f0, cur, 2);
+      DMH_MM(f1);
+      DMH_RD(f1, cur, 3);
+      DMH_MM(f0);
+      DMH_MM(f1);
+      DMH_SCHED_SUB();
+      DMH_SCHED_SUB();
+      DMH_SCHED_SUB();
+      __builtin_amdgcn_sched_group_barrier(0x008, BM * BN, 0);
+    }
+
+    // ---- epilogue (per wave, no workgroup barrier) ----------------------------
+    // The wave's 128 x 64 output goes out one 32 x 64 block row at a time through
+    // its 4 KB staging area:
+    //   phase 1  acc -> staging: v = bf16(acc) (bf16(c * acc) for POLY)
+    //   phase 2  row-major pass, 16-byte chunks: POLY epilogue (aux read in 16 B,
+    //            written back for phase 3), store C[i][j]
+    //   phase 3  transposed pass: 8 rows x 4 columns per lane, transposed in
+    //            registers, store C^T[j][i] in 16-byte chunks
+    // Staging element (r, c) sits at byte r*128 + 16*((c>>3) ^ (r&7)) + 2*(c&7): the
+    // accesses of all three phases spread over every bank.  acc[i][j][4g+q] holds
+    // C[32 i + (lane&31)][32 j + 8g + 4(lane>>5) + q] of the wave tile.
+    // Symmetric products (upper tiles only): off-diagonal tiles store both C and
+    // C^T; on a diagonal tile only the elements with i <= j are stored, once
+    // row-major and once transposed, so the lower triangle takes the upper one's
+    // values exactly.
+    {
+      const int wi0 = ti * TILE + WT_M * wm, wj0 = tj * TILE + WT_N * wn;
+      const bool diag = g.sym && ti == tj;
+      bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
+      bf16* outtb = g.outT ? g.outT + (long long)b * g.outT_bs : nullptr;
+      const bool al_out = (g.out_ld & 7) == 0, al_outT = (g.outT_ld & 7) == 0;
+      const bf16* auxb = EPI == EPI_POLY ? g.aux + (long long)b * g.aux_bs : nullptr;
+      // POLY: the aux of block rows 0 and 1 is requested up front and that of row
+      // bi+2 once row bi's accumulators are drained, so the reads run two block rows
+      // ahead of their use (latency hidden, registers bounded)
+      constexpr int AUX_AHEAD = 2;
+      bf16x8 av[EPI == EPI_POLY ? BM : 1][4];
+      auto load_aux = [&](int bi) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int u = lane + 64 * v;
+          const int gi = wi0 + 32 * bi + (u >> 3), gj = wj0 + 8 * (u & 7);
+          av[bi][v] = *(const bf16x8*)(auxb + (long long)gi * g.aux_ld + gj);
+        }
+      };
+      if (EPI == EPI_POLY) {
+#pragma unroll
+        for (int bi = 0; bi < AUX_AHEAD; ++bi) load_aux(bi);
+      }
+#pragma unroll
+      for (int bi = 0; bi < BM; ++bi) {
+        const int i0 = wi0 + 32 * bi;   // global row of staging row 0
+        // phase 1
+#pragma unroll
+        for (int bj = 0; bj < BN; ++bj) {
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            bf16x4 o;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float v = acc[bi][bj][4 * gq + q];
+              o[q] = f2bf(EPI == EPI_POLY ? g.beta * v : v);
+            }
+            const int ch = 4 * bj + gq;
+            *(bf16x4*)(stg + r32 * 128 + 16 * (ch ^ (r32 & 7)) + 8 * hi) = o;
+          }
+        }
+        if (EPI == EPI_POLY && bi + AUX_AHEAD < BM) load_aux(bi + AUX_AHEAD);
+        // phase 2
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int u = lane + 64 * v;
+          const int r = u >> 3, ch = u & 7;
+          char* lp = stg + r * 128 + 16 * (ch ^ (r & 7));
+          bf16x8 val = *(const bf16x8*)lp;
+          const int gi = i0 + r, gj = wj0 + 8 * ch;
+          if (EPI == EPI_POLY) {
+            const int qd = diag && gi < g.diag_lim ? gi - gj : -1;   // the diagonal's slot, if here
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+              val[q] = f2bf(g.alpha * bf2f(av[EPI == EPI_POLY ? bi : 0][v][q]) + bf2f(val[q]) +
+                            (q == qd ? g.diag_add : 0.f));
+            if (outtb) *(bf16x8*)lp = val;
+          }
+          if (outb && gi < g.valid_i) {
+            unsigned mask = 0xffu;
+            if (gj + 8 > g.valid_j) mask = gj >= g.valid_j ? 0u : (1u << (g.valid_j - gj)) - 1u;
+            if (diag) {   // keep j >= i
+              const int d = gi - gj;   // elements q >= d
+              mask &= d <= 0 ? 0xffu : (d >= 8 ? 0u : (0xffu << d) & 0xffu);
+            }
+            if (mask) store8(outb + (long long)gi * g.out_ld + gj, val, mask, al_out);
+          }
+        }
+        // phase 3
+        if (outtb) {
+          const int a = lane & 3, c = lane >> 2;   // rows 8a..8a+7, columns 4c..4c+3
+          uint2 rr[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int r = 8 * a + q;
+            rr[q] = *(const uint2*)(stg + r * 128 + 16 * ((c >> 1) ^ (r & 7)) + 8 * (c & 1));
+          }
+          const int gi = i0 + 8 * a;
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) {
+            const int gj = wj0 + 4 * c + cc;
+            // column cc of the 8x4 block: halves (cc&1) of words (cc>>1)
+            uint32_t w[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+              const uint32_t x0 = (cc >> 1) ? rr[2 * h].y : rr[2 * h].x;
+              const uint32_t x1 = (cc >> 1) ? rr[2 * h + 1].y : rr[2 * h + 1].x;
+              const uint32_t lo = (cc & 1) ? (x0 >> 16) : (x0 & 0xffffu);
+              const uint32_t hw = (cc & 1) ? (x1 & 0xffff0000u) : (x1 << 16);
+              w[h] = lo | hw;
+            }
+            if (gj >= g.valid_j) continue;
+            unsigned mask = 0xffu;
+            if (gi + 8 > g.valid_i) mask = gi >= g.valid_i ? 0u : (1u << (g.valid_i - gi)) - 1u;
+            if (diag) {   // keep i <= j
+              const int d = gj - gi;   // elements q <= d
+              mask &= d < 0 ? 0u : (d >= 7 ? 0xffu : (1u << (d + 1)) - 1u);
+            }
+            if (mask) {
+              const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
+              store8(outtb + (long long)gj * g.outT_ld + gi, __builtin_bit_cast(bf16x8, wv), mask,
+                     al_outT);
+            }
+          }
+        }
+      }
+    }
+    if (!more) break;
+    lid = nlid; b = nb; ti = nti; tj = ntj;
+    rP = rPn; rQ = rQn;
+    s_cur ^= 1;
   }
 #undef DMH_RD
 #undef DMH_MM
 #undef DMH_SCHED_SUB
 #undef DMH_GLOAD
-  // the re-fetches past the last stage may still be landing in LDS
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  // ---- epilogue -------------------------------------------------------------
-  // The 256x256 output tile is staged through LDS as bf16 (the whole 128 KB),
-  // so both output layouts leave in 16-byte coalesced stores.
-  //   phase 1  acc -> LDS: v = bf16(acc) (bf16(c * acc) for POLY)
-  //   phase 2  row-major pass: POLY epilogue (aux read in 16 B), store C[i][j]
-  //   phase 3  transposed pass: 8 rows x 4 columns per step, transposed in
-  //            registers, store C^T[j][i]
-  // LDS element (i, j) of the tile sits at byte i*512 + 16*((j>>3) ^ swz(i)) + 2*(j&7);
-  // swz(i) = ((i>>3)&3) | ((((i&7) ^ (i>>5)) & 7) << 2) keeps 32 consecutive rows (phase
-  // 1) and rows 8 apart (phase 3) on distinct 16-byte slots.
-  // acc[i][j][4g+q] holds C[i0 + (lane&31)][j0 + 8g + 4(lane>>5) + q].
-  // The barriers below only order LDS (lgkmcnt), so the aux tile, fetched in one
-  // batch up front, stays in flight while the accumulators drain.
-  const int gi0 = ti * TILE, gj0 = tj * TILE;
-  constexpr int NU = TILE * TILE / 8 / GEMM_THREADS;   // 16-byte chunks per thread
-  bf16x8 av[NU];
-  if (EPI == EPI_POLY) {
-    const bf16* auxb = g.aux + (long long)b * g.aux_bs + (long long)gi0 * g.aux_ld + gj0;
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const int e = tid + GEMM_THREADS * u;
-      av[u] = *(const bf16x8*)(auxb + (long long)(e >> 5) * g.aux_ld + (e & 31) * 8);
-    }
-  }
-  ring_barrier();
-  char* const cs = smem;
-  auto cswz = [](int i) { return ((i >> 3) & 3) | ((((i & 7) ^ (i >> 5)) & 7) << 2); };
-  auto caddr = [&](int i, int j) { return i * 512 + 16 * ((j >> 3) ^ cswz(i)) + 2 * (j & 7); };
-#pragma unroll
-  for (int bi = 0; bi < BM; ++bi) {
-    const int il = WT_M * wm + 32 * bi + r32;
-#pragma unroll
-    for (int bj = 0; bj < BN; ++bj) {
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int jl = WT_N * wn + 32 * bj + 8 * gq + 4 * (lane >> 5);
-        bf16x4 o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float v = acc[bi][bj][4 * gq + q];
-          o[q] = f2bf(EPI == EPI_POLY ? g.beta * v : v);
-        }
-        *(bf16x4*)(cs + caddr(il, jl)) = o;
-      }
-    }
-  }
-  ring_barrier();
-  const bool diag = g.sym && ti == tj;
-  if (diag) {
-    // exact symmetry: the lower triangle of a diagonal tile takes the upper one's
-    // values.  8x8 blocks (I, J), I >= J: block (J, I) is read as 8 rows of 16 B,
-    // transposed in registers and written over block (I, J); on the diagonal
-    // blocks only the strictly lower elements are replaced.  Reads and writes of
-    // one thread touch blocks no other thread writes.
-    for (int blk = tid; blk < 32 * 33 / 2; blk += GEMM_THREADS) {
-      int I = (int)((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
-      while ((I + 1) * (I + 2) / 2 <= blk) ++I;
-      while (I * (I + 1) / 2 > blk) --I;
-      const int J = blk - I * (I + 1) / 2;
-      bf16x8 src[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) src[r] = *(const bf16x8*)(cs + caddr(8 * J + r, 8 * I));
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        bf16x8 d;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) d[r] = src[r][c];
-        if (I == J) {
-#pragma unroll
-          for (int r = 0; r < 8; ++r)
-            if (r >= c) d[r] = src[c][r];
-        }
-        *(bf16x8*)(cs + caddr(8 * I + c, 8 * J)) = d;
-      }
-    }
-    ring_barrier();
-  }
-  const bool need_t = g.outT && (!g.sym || !diag);
-  bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
-#pragma unroll
-  for (int u = 0; u < NU; ++u) {
-    const int e = tid + GEMM_THREADS * u;
-    const int il = e >> 5, jc = (e & 31) * 8;
-    char* lp = cs + il * 512 + 16 * ((jc >> 3) ^ cswz(il));
-    bf16x8 v = *(const bf16x8*)lp;
-    const int gi = gi0 + il, gj = gj0 + jc;
-    if (EPI == EPI_POLY) {
-      const int qd = diag && gi < g.diag_lim ? il - jc : -1;   // the diagonal's slot, if here
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        v[q] = f2bf(g.alpha * bf2f(av[u][q]) + bf2f(v[q]) + (q == qd ? g.diag_add : 0.f));
-      if (need_t) *(bf16x8*)lp = v;
-    }
-    if (outb && gi < g.valid_i) {
-      bf16* op = outb + (long long)gi * g.out_ld + gj;
-      if (gj + 7 < g.valid_j && (g.out_ld & 7) == 0) {
-        *(bf16x8*)op = v;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          if (gj + q < g.valid_j) op[q] = v[q];
-      }
-    }
-  }
-  if (!need_t) return;
-  ring_barrier();
-  bf16* outtb = g.outT + (long long)b * g.outT_bs;
-  for (int u = 0; u < TILE * TILE / 32 / GEMM_THREADS; ++u) {
-    const int e = tid + GEMM_THREADS * u;
-    const int ic = (e & 31) * 8, jg = (e >> 5) * 4;   // rows ic..ic+7, columns jg..jg+3
-    uint2 r[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) r[q] = *(const uint2*)(cs + caddr(ic + q, jg));
-    const int gi = gi0 + ic;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int gj = gj0 + jg + c;
-      // column c of the 8x4 block: halves (c&1) of words (c>>1)
-      uint32_t w[4];
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const uint32_t x0 = (c >> 1) ? r[2 * h].y : r[2 * h].x;
-        const uint32_t x1 = (c >> 1) ? r[2 * h + 1].y : r[2 * h + 1].x;
-        const uint32_t lo = (c & 1) ? (x0 >> 16) : (x0 & 0xffffu);
-        const uint32_t hi = (c & 1) ? (x1 & 0xffff0000u) : (x1 << 16);
-        w[h] = lo | hi;
-      }
-      if (gj >= g.valid_j) continue;
-      bf16* tp = outtb + (long long)gj * g.outT_ld + gi;
-      if (gi + 7 < g.valid_i && (g.outT_ld & 7) == 0) {
-        *(uint4*)tp = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          if (gi + q < g.valid_i) {
-            const uint16_t bits = (uint16_t)((w[q >> 1] >> (16 * (q & 1))) & 0xffffu);
-            tp[q] = __builtin_bit_cast(bf16, bits);
-          }
-        }
-      }
-    }
-  }
 }
-
 // ---------------------------------------------------------------------------
 // entry: Frobenius norm partials, then scale + cast + pack into padded T and W
 // ---------------------------------------------------------------------------
@@ -470,12 +580,12 @@ __global__ __launch_bounds__(256) void entry_norm_partials(InView v, double* par
   if (threadIdx.x == 0) partials[b * NORM_CHUNKS + chunk] = red[0];
 }
 
-// Pack 64x64 tiles of T-space (i < np rows, j < mp cols).  in_tall: the input is
-// T (rows = n); otherwise it is W (rows = m) and is transposed on the way.
+// Pack 64x64 tiles of T (i < np rows, j < mp cols).  in_tall: the input is T
+// (rows = n); otherwise it is W = T^T (rows = m) and is transposed on the way.
 // scale_mode: 0 none, 1: 1/(||x||+1e-7), 2: 1/(1.01||x||+1e-7).
 __global__ __launch_bounds__(256) void entry_pack(InView v, int in_tall, int scale_mode,
                                                   const double* partials, int n, int m,
-                                                  int np, int mp, bf16* T, bf16* W) {
+                                                  int np, int mp, bf16* T) {
   __shared__ float tile[64][65];
   const int b = blockIdx.z;
   const int i0 = blockIdx.y * 64, j0 = blockIdx.x * 64;
@@ -508,12 +618,9 @@ __global__ __launch_bounds__(256) void entry_pack(InView v, int in_tall, int sca
   }
   __syncthreads();
   bf16* Tb = T + (long long)b * np * mp;
-  bf16* Wb = W + (long long)b * mp * np;
   for (int rr = ty; rr < 64; rr += 4) {
     const float xt = scale_mode ? tile[rr][tx] / scale : tile[rr][tx];
     Tb[(long long)(i0 + rr) * mp + j0 + tx] = f2bf(xt);
-    const float xw = scale_mode ? tile[tx][rr] / scale : tile[tx][rr];
-    Wb[(long long)(j0 + rr) * np + i0 + tx] = f2bf(xw);
   }
 }
 
@@ -544,27 +651,44 @@ ChainWs chain_ws(void* ws, int batch, const ChainDims& d) {
   const size_t tw = (size_t)batch * d.np * d.mp;
   const size_t sq = (size_t)batch * d.mp * d.mp;
   const size_t part = (size_t)batch * NORM_CHUNKS * sizeof(double);
-  w.bytes = (4 * tw + 2 * sq) * sizeof(bf16) + ((part + 255) / 256) * 256;
+  w.bytes = (2 * tw + 2 * sq) * sizeof(bf16) + ((part + 255) / 256) * 256;
   if (!ws) return w;
   w.T0 = (bf16*)ws;
-  w.W0 = w.T0 + tw;
-  w.T1 = w.W0 + tw;
-  w.W1 = w.T1 + tw;
-  w.A = w.W1 + tw;
+  w.T1 = w.T0 + tw;
+  w.A = w.T1 + tw;
   w.B = w.A + sq;
   w.partials = (double*)(w.B + sq);
   return w;
 }
 
-template <int EPI>
-static int launch_gemm(const GemmArgs& g, int batch, hipStream_t stream, const char* what) {
-  const int per = g.sym ? g.tiles_m * (g.tiles_m + 1) / 2 : g.tiles_m * g.tiles_n;
-  const long long blocks = (long long)per * batch;
-  if (blocks <= 0 || blocks > 0x7fffffffLL) {
-    set_error("%s: bad grid (%lld blocks)", what, blocks);
+// compute units of the current device (one persistent GEMM workgroup each)
+static int device_cus() {
+  constexpr int MAXDEV = 64;
+  static int cus[MAXDEV];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <int EPI, int TNL>
+static int launch_gemm(GemmArgs g, int batch, hipStream_t stream, const char* what) {
+  const long long per = g.sym ? (long long)g.tiles_m * (g.tiles_m + 1) / 2
+                              : (long long)g.tiles_m * g.tiles_n;
+  const long long tiles = per * batch;
+  const int cus = device_cus();
+  if (tiles <= 0 || tiles > 0x7fffffffLL || cus <= 0) {
+    set_error("%s: bad grid (%lld tiles, %d compute units)", what, tiles, cus);
     return DMH_EINVAL;
   }
-  hipLaunchKernelGGL(gemm_nt_bf16<EPI>, dim3((unsigned)blocks), dim3(GEMM_THREADS), 0, stream, g);
+  g.total_tiles = (int)tiles;
+  g.batch = batch;
+  const int grid = (int)(tiles < cus ? tiles : cus);
+  hipLaunchKernelGGL((gemm_nt_bf16<EPI, TNL>), dim3(grid), dim3(GEMM_THREADS), 0, stream, g);
   DMH_CHECK_LAUNCH(what);
   return DMH_OK;
 }
@@ -580,7 +704,12 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     return DMH_OK;
   }
   const int tm = d.mp / TILE, tn = d.np / TILE;
-  bf16 *Tc = w.T0, *Wc = w.W0, *Tn = w.T1, *Wn = w.W1;
+  // Consecutive launches walk the batch in opposite directions, so each one starts
+  // on the matrices the previous one wrote last, which are still in the memory-side
+  // cache (the group's operands are several times its size).  The entry pack wrote
+  // the batch in increasing order, so K1 of the first iteration runs reversed.
+  int rev = 1;
+  bf16 *Tc = w.T0, *Tn = w.T1;
   bf16 *Am = w.A, *Bm = w.B;
   for (int it = 0; it < steps; ++it) {
     const float a = (float)coeffs[3 * it + 0];
@@ -588,15 +717,17 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     const float c = (float)coeffs[3 * it + 2];
     const bool last = it + 1 == steps;
     int rc;
-    // K1: A = W W^T
+    // K1: A = W W^T = T^T T, with both operands read K-major from T (row k of T
+    // holds column k of W)
     GemmArgs g1{};
-    g1.P = Wc; g1.p_bs = (long long)d.mp * d.np; g1.p_ld = d.np;
-    g1.Q = Wc; g1.q_bs = g1.p_bs; g1.q_ld = d.np;
+    g1.P = Tc; g1.p_bs = (long long)d.np * d.mp; g1.p_ld = d.mp;
+    g1.Q = Tc; g1.q_bs = g1.p_bs; g1.q_ld = d.mp;
     g1.K = d.np; g1.tiles_m = tm; g1.tiles_n = tm; g1.sym = 1;
     g1.out = Am; g1.out_bs = (long long)d.mp * d.mp; g1.out_ld = d.mp;
     g1.outT = Am; g1.outT_bs = g1.out_bs; g1.outT_ld = d.mp;
     g1.valid_i = d.mp; g1.valid_j = d.mp;
-    if ((rc = launch_gemm<EPI_STORE>(g1, batch, stream, "ns K1 (W W^T)"))) return rc;
+    g1.rev = rev; rev ^= 1;
+    if ((rc = launch_gemm<EPI_STORE, 1>(g1, batch, stream, "ns K1 (T^T T)"))) return rc;
     // K2: B = b A + c A A
     GemmArgs g2 = g1;
     g2.P = Am; g2.p_bs = (long long)d.mp * d.mp; g2.p_ld = d.mp;
@@ -605,15 +736,15 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     g2.alpha = bcoef; g2.beta = c; g2.diag_add = a; g2.diag_lim = d.m;
     g2.aux = Am; g2.aux_bs = g2.p_bs; g2.aux_ld = d.mp;
     g2.out = Bm; g2.outT = Bm;
-    if ((rc = launch_gemm<EPI_POLY>(g2, batch, stream, "ns K2 (bA + cA^2 + aI)"))) return rc;
-    // K3: T' = T B'  (and W' = T'^T)
+    g2.rev = rev; rev ^= 1;
+    if ((rc = launch_gemm<EPI_POLY, 0>(g2, batch, stream, "ns K2 (bA + cA^2 + aI)"))) return rc;
+    // K3: T' = T B' (the final iterate in the caller's orientation)
     GemmArgs g3{};
     g3.P = Tc; g3.p_bs = (long long)d.np * d.mp; g3.p_ld = d.mp;
     g3.Q = Bm; g3.q_bs = (long long)d.mp * d.mp; g3.q_ld = d.mp;
     g3.K = d.mp; g3.tiles_m = tn; g3.tiles_n = tm; g3.sym = 0;
     if (!last) {
       g3.out = Tn; g3.out_bs = g3.p_bs; g3.out_ld = d.mp;
-      g3.outT = Wn; g3.outT_bs = (long long)d.mp * d.np; g3.outT_ld = d.np;
       g3.valid_i = d.np; g3.valid_j = d.mp;
     } else if (orient_tall) {
       g3.out = outp; g3.out_bs = (long long)d.n * d.m; g3.out_ld = d.m;
@@ -622,9 +753,9 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
       g3.outT = outp; g3.outT_bs = (long long)d.n * d.m; g3.outT_ld = d.n;
       g3.valid_i = d.n; g3.valid_j = d.m;
     }
-    if ((rc = launch_gemm<EPI_STORE>(g3, batch, stream, "ns K3 (T B')"))) return rc;
+    g3.rev = rev; rev ^= 1;
+    if ((rc = launch_gemm<EPI_STORE, 0>(g3, batch, stream, "ns K3 (T B')"))) return rc;
     bf16* t = Tc; Tc = Tn; Tn = t;
-    t = Wc; Wc = Wn; Wn = t;
   }
   return DMH_OK;
 }
@@ -671,7 +802,7 @@ int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int 
     DMH_CHECK_LAUNCH("entry_norm_partials");
   }
   hipLaunchKernelGGL(entry_pack, dim3(d.mp / 64, d.np / 64, batch), dim3(256), 0, stream, v,
-                     orient_tall, entry_mode, w.partials, d.n, d.m, d.np, d.mp, w.T0, w.W0);
+                     orient_tall, entry_mode, w.partials, d.n, d.m, d.np, d.mp, w.T0);
   DMH_CHECK_LAUNCH("entry_pack");
   return chain_run_packed(stream, w, batch, d, orient_tall, coeffs, steps, (bf16*)out);
 }

@@ -1501,7 +1501,7 @@ int dmh_deflated_polar(hipStream_t stream, const float* A, const float* Omega, i
   int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, k, d, w);
   if (rc) return rc;
   // X0 goes straight into the chain's packed operands (T and W = T^T)
-  if ((rc = launch_restore(stream, A, batch, n, m, w, d, nullptr, 0, cw.T0, cw.W0, cd.np, cd.mp)))
+  if ((rc = launch_restore(stream, A, batch, n, m, w, d, nullptr, 0, cw.T0, nullptr, cd.np, cd.mp)))
     return rc;
   if (chain_event && hipEventRecord((hipEvent_t)chain_event, stream) != hipSuccess) {
     set_error("dmh_deflated_polar: hipEventRecord failed");
