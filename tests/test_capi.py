@@ -35,7 +35,8 @@ def test_ns_workspace_size(lib):
     n = ctypes.c_size_t()
     assert lib.dmh_ns_workspace_size(2, 300, 700, 0, ctypes.byref(n)) == 0
     mp, np_ = 512, 768          # 300 -> 512, 700 -> 768 (256 tiles)
-    want = 4 * 2 * np_ * mp * 2 + 2 * 2 * mp * mp * 2 + 256 * ((2 * 64 * 8 + 255) // 256)
+    # T double-buffered (2 x np x mp), A and B' (mp x mp), bf16; fp64 norm partials
+    want = 2 * 2 * np_ * mp * 2 + 2 * 2 * mp * mp * 2 + 256 * ((2 * 64 * 8 + 255) // 256)
     assert n.value == want
     assert lib.dmh_ns_workspace_size(1, 0, 5, 0, ctypes.byref(n)) == 1
     assert b"bad arguments" in lib.dmh_last_error()
