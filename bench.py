@@ -70,25 +70,23 @@ def make_inputs(groups, device, seed=1234, kind="spiked"):
 
 def polar_step(fac, stacks, bd_step, ns_steps, events=None):
     """One polar step over all groups, as the optimizer runs it
-    (_DeflatedPolarBase.polar_group: clip + iteration); returns per-group (U, k).
-    With `events`, HIP events on the launch stream bracket each group and mark
-    the start of its NS chain."""
+    (_DeflatedPolarBase.polar_groups: the groups' clips, then their iterations);
+    returns per-group (U, k).  With `events`, appends a list of (start, end) HIP
+    event pairs recorded on the launch stream around each group's NS chain."""
     import torch
     from defmuon_amd.optim import deflation_batched as DB
-    outs = []
+    gens = []
     for gi, A in enumerate(stacks):
         gen = torch.Generator(device=A.device)
         gen.manual_seed((bd_step * 1009 + gi * 9176867) % (2 ** 62))
-        ev = None
-        if events is not None:
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-            ev[1].record()   # creates the HIP event; the library re-records it mid-call
-            ev[0].record()
-        U, kvec, _ = fac.polar_group(A, generator=gen, steps=ns_steps,
-                                     chain_event=None if ev is None else ev[1])
-        if ev is not None:
-            ev[2].record()
-            events.append(ev)
+        gens.append(gen)
+    evs = None
+    if events is not None:
+        evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in stacks]
+        events.append(evs)
+    res = fac.polar_groups(stacks, gens, steps=ns_steps, chain_events=evs)
+    outs = []
+    for A, (U, kvec, _) in zip(stacks, res):
         if DB._GATE_ACC[0] is None:
             DB._GATE_ACC[0] = torch.zeros(3, dtype=torch.int64, device=A.device)
         DB._GATE_ACC[0] += torch.stack([
@@ -215,8 +213,8 @@ def main():
     wall = time.perf_counter() - t0
     gpu_ms = start.elapsed_time(stop)
     ms_per_step = gpu_ms / args.steps
-    ns_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
-    front_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
+    ns_ms = sum(e0.elapsed_time(e1) for evs in events for e0, e1 in evs) / args.steps
+    front_ms = ms_per_step - ns_ms   # the groups' front-ends (concurrent) and the gate ticks
     st = DB.polar_stats()
     flops = ns_flops(groups)
     achieved = flops / (ns_ms * 1e-3) / 1e12

@@ -109,6 +109,22 @@ int dmh_deflated_polar(dmh_stream_t stream, const float* A, const float* Omega, 
                        int qr_passes, const double* coeffs, int steps, void* out, long long* k,
                        float* d, void* ws, size_t ws_bytes, void* chain_event);
 
+/* The two halves of dmh_deflated_polar, on one workspace of
+ * dmh_deflated_polar_workspace_size, so that the front-ends of several shape
+ * groups can run on separate streams before their chains (muon.py:283-312 runs the
+ * groups one after the other; each group's result is the same either way).
+ *   _front: BATCHED_CLIP (deflation_batched.py:155-189) with X0 left, bf16, in the
+ *           chain's packed operand inside ws; writes k and d.
+ *   _chain: the bf16 iteration (deflation_batched.py:196-211 via muon.py:310-312)
+ *           from that operand, same batch/n/m, to out (batch, n, m) bf16.
+ * ws must stay untouched between the two calls (stream-ordered). */
+int dmh_deflated_polar_front(dmh_stream_t stream, const float* A, const float* Omega, int batch,
+                             int n, int m, int r, int kw, float ratio, float thresh, float pad,
+                             int niter, int qr_passes, long long* k, float* d, void* ws,
+                             size_t ws_bytes);
+int dmh_deflated_polar_chain(dmh_stream_t stream, int batch, int n, int m, const double* coeffs,
+                             int steps, void* out, void* ws, size_t ws_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1476,6 +1476,54 @@ int dmh_rmfro_clip(hipStream_t stream, const float* A, const float* Omega, int b
                         0);
 }
 
+// Front-end half of dmh_deflated_polar: rSVD, gate and d, and the deflated entry
+// X0 written (bf16) straight into the chain's packed operand inside ws.
+int dmh_deflated_polar_front(hipStream_t stream, const float* A, const float* Omega, int batch,
+                             int n, int m, int r, int kw, float ratio, float thresh, float pad,
+                             int niter, int qr_passes, long long* k, float* d, void* ws,
+                             size_t ws_bytes) {
+  if (batch == 0) return DMH_OK;
+  // ws stands in for the output pointer: the entry goes into the workspace
+  if (clip_args("dmh_deflated_polar_front", A, Omega, ws, k, d, batch, n, m, r, kw, niter,
+                qr_passes, pad))
+    return DMH_EINVAL;
+  size_t chain_off = 0;
+  const size_t need = fused_bytes(batch, n, m, &chain_off);
+  if (!ws || ws_bytes < need) {
+    set_error("dmh_deflated_polar_front: workspace %zu < %zu bytes", ws_bytes, need);
+    return DMH_EWORKSPACE;
+  }
+  RsvdWs w = rsvd_layout(ws, batch, n, m);
+  const ChainDims cd = chain_dims(n, m, 1);
+  const ChainWs cw = chain_ws((char*)ws + chain_off, batch, cd);
+  GateParams gp{r, kw, ratio, thresh, pad};
+  int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, k, d, w);
+  if (rc) return rc;
+  return launch_restore(stream, A, batch, n, m, w, d, nullptr, 0, cw.T0, nullptr, cd.np, cd.mp);
+}
+
+// Chain half of dmh_deflated_polar: `steps` iterations from the entry that
+// dmh_deflated_polar_front left in ws (same batch, n, m), polar factors to out
+// (batch, n, m) bf16.
+int dmh_deflated_polar_chain(hipStream_t stream, int batch, int n, int m, const double* coeffs,
+                             int steps, void* out, void* ws, size_t ws_bytes) {
+  if (batch == 0) return DMH_OK;
+  if (batch < 0 || n < m || m <= 0 || !out || steps < 0 || (steps > 0 && !coeffs)) {
+    set_error("dmh_deflated_polar_chain: bad arguments (batch=%d n=%d m=%d steps=%d)", batch, n,
+              m, steps);
+    return DMH_EINVAL;
+  }
+  size_t chain_off = 0;
+  const size_t need = fused_bytes(batch, n, m, &chain_off);
+  if (!ws || ws_bytes < need) {
+    set_error("dmh_deflated_polar_chain: workspace %zu < %zu bytes", ws_bytes, need);
+    return DMH_EWORKSPACE;
+  }
+  const ChainDims cd = chain_dims(n, m, 1);
+  const ChainWs cw = chain_ws((char*)ws + chain_off, batch, cd);
+  return chain_run_packed(stream, cw, batch, cd, 1, coeffs, steps, (bf16*)out);
+}
+
 int dmh_deflated_polar(hipStream_t stream, const float* A, const float* Omega, int batch, int n,
                        int m, int r, int kw, float ratio, float thresh, float pad, int niter,
                        int qr_passes, const double* coeffs, int steps, void* out, long long* k,
@@ -1488,26 +1536,14 @@ int dmh_deflated_polar(hipStream_t stream, const float* A, const float* Omega, i
     set_error("dmh_deflated_polar: bad steps/coeffs (steps=%d)", steps);
     return DMH_EINVAL;
   }
-  size_t chain_off = 0;
-  const size_t need = fused_bytes(batch, n, m, &chain_off);
-  if (!ws || ws_bytes < need) {
-    set_error("dmh_deflated_polar: workspace %zu < %zu bytes", ws_bytes, need);
-    return DMH_EWORKSPACE;
-  }
-  RsvdWs w = rsvd_layout(ws, batch, n, m);
-  const ChainDims cd = chain_dims(n, m, 1);
-  const ChainWs cw = chain_ws((char*)ws + chain_off, batch, cd);
-  GateParams gp{r, kw, ratio, thresh, pad};
-  int rc = rsvd_core(stream, A, Omega, batch, n, m, r, niter, qr_passes, gp, k, d, w);
+  int rc = dmh_deflated_polar_front(stream, A, Omega, batch, n, m, r, kw, ratio, thresh, pad,
+                                    niter, qr_passes, k, d, ws, ws_bytes);
   if (rc) return rc;
-  // X0 goes straight into the chain's packed operands (T and W = T^T)
-  if ((rc = launch_restore(stream, A, batch, n, m, w, d, nullptr, 0, cw.T0, nullptr, cd.np, cd.mp)))
-    return rc;
   if (chain_event && hipEventRecord((hipEvent_t)chain_event, stream) != hipSuccess) {
     set_error("dmh_deflated_polar: hipEventRecord failed");
     return DMH_ELAUNCH;
   }
-  return chain_run_packed(stream, cw, batch, cd, 1, coeffs, steps, (bf16*)out);
+  return dmh_deflated_polar_chain(stream, batch, n, m, coeffs, steps, out, ws, ws_bytes);
 }
 
 }  // extern "C"

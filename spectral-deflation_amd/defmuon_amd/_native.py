@@ -43,6 +43,12 @@ _SIGS = {
                                    c_float, c_float, c_int, c_int,
                                    ctypes.POINTER(ctypes.c_double), c_int, c_vp, c_vp, c_vp,
                                    c_vp, c_sz, c_vp]),
+    "dmh_deflated_polar_front": (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int,
+                                         c_float, c_float, c_float, c_int, c_int, c_vp, c_vp,
+                                         c_vp, c_sz]),
+    "dmh_deflated_polar_chain": (c_int, [c_vp, c_int, c_int, c_int,
+                                         ctypes.POINTER(ctypes.c_double), c_int, c_vp, c_vp,
+                                         c_sz]),
 }
 
 # largest sketch width the front-end kernels carry (include/defmuon_hip.h)
@@ -240,3 +246,49 @@ def deflated_polar(A, Omega, kw, ratio, thresh, pad, coeffs, niter=1, passes=1,
                                   c_vp(chain_event.cuda_event if chain_event is not None else 0)),
            "dmh_deflated_polar")
     return out, k, d
+
+
+class PolarFront:
+    """A deflated front-end result waiting for its chain: the workspace (holding
+    the packed bf16 entry X0), the gate widths k and divisors d, and the shape."""
+    __slots__ = ("ws", "nbytes", "k", "d", "shape", "device")
+
+    def __init__(self, ws, nbytes, k, d, shape, device):
+        self.ws, self.nbytes, self.k, self.d, self.shape, self.device = ws, nbytes, k, d, shape, device
+
+
+def deflated_polar_front(A, Omega, kw, ratio, thresh, pad, niter=1, passes=1):
+    """Front-end half of deflated_polar on the current stream: returns a
+    PolarFront for deflated_polar_chain."""
+    A, Omega = _f32c(A, "deflated_polar_front"), _f32c(Omega, "deflated_polar_front")
+    B, n, m = A.shape
+    r = Omega.shape[-1]
+    k = torch.empty((B,), dtype=torch.int64, device=A.device)
+    d = torch.empty((B,), dtype=torch.float32, device=A.device)
+    lib = load()
+    nbytes = c_sz()
+    _check(lib.dmh_deflated_polar_workspace_size(B, n, m, r, ctypes.byref(nbytes)),
+           "dmh_deflated_polar_workspace_size")
+    ws = _workspace(max(nbytes.value, 1), A.device)
+    if B:
+        _check(lib.dmh_deflated_polar_front(_stream(A.device), _ptr(A), _ptr(Omega), B, n, m, r,
+                                            int(kw), float(ratio), float(thresh), float(pad),
+                                            int(niter), int(passes), _ptr(k), _ptr(d), _ptr(ws),
+                                            nbytes.value),
+               "dmh_deflated_polar_front")
+    return PolarFront(ws, nbytes.value, k, d, (B, n, m), A.device)
+
+
+def deflated_polar_chain(front, coeffs):
+    """Chain half of deflated_polar on the current stream: the polar factors
+    (B, n, m) bf16 from a PolarFront."""
+    B, n, m = front.shape
+    out = torch.empty((B, n, m), dtype=torch.bfloat16, device=front.device)
+    if B == 0:
+        return out
+    steps = len(coeffs)
+    flat = (ctypes.c_double * max(3 * steps, 1))(*[float(v) for t in coeffs for v in t])
+    _check(load().dmh_deflated_polar_chain(_stream(front.device), B, n, m, flat, steps,
+                                           _ptr(out), _ptr(front.ws), front.nbytes),
+           "dmh_deflated_polar_chain")
+    return out

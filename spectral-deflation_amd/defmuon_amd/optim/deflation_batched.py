@@ -163,6 +163,16 @@ class _DeflatedPolarBase:
         """The (a, b, c) triples `_iterate` applies, or None if unknown."""
         return None
 
+    def _fused(self, steps):
+        """The schedule when this arm's clip and iteration are the library's own
+        (so both can run as one library call), else None."""
+        cls = type(self)
+        hs = self.schedule(steps)
+        if (hs is not None and cls.BATCHED_CLIP is _DeflatedPolarBase.BATCHED_CLIP
+                and cls._iterate in (DeflatedNSPolar._iterate, DeflatedPEPolar._iterate)):
+            return hs
+        return None
+
     def polar_group(self, A, generator=None, steps=5, Omega=None, chain_event=None):
         """BATCHED_CLIP(A, bf16) then `_iterate` for one tall shape group, as
         muon.py:298,310-312 run them.  For the built-in arms both run in one
@@ -170,11 +180,8 @@ class _DeflatedPolarBase:
         layout; an arm that overrides BATCHED_CLIP or `_iterate` gets exactly its
         own two calls.  Returns (polar factors (B, n, m) bf16, k, d).  chain_event
         (fused path only): a torch.cuda.Event recorded between the two phases."""
-        cls = type(self)
-        hs = self.schedule(steps)
-        fused = (hs is not None and cls.BATCHED_CLIP is _DeflatedPolarBase.BATCHED_CLIP
-                 and cls._iterate in (DeflatedNSPolar._iterate, DeflatedPEPolar._iterate))
-        if not fused:
+        hs = self._fused(steps)
+        if hs is None:
             X0, k, d = self.BATCHED_CLIP(A, generator=generator, Omega=Omega, pad=self.PAD,
                                          out_dtype=torch.bfloat16)
             return self._iterate(X0, steps), k, d
@@ -184,6 +191,73 @@ class _DeflatedPolarBase:
             Omega = torch.randn(Bn, m, r, device=A.device, dtype=A.dtype, generator=generator)
         return _native.deflated_polar(A, Omega, kw, GATE_RATIO, DEFLATE_THRESH, self.PAD, hs,
                                       RSVD_NITER, CHOLQR_PASSES, chain_event)
+
+    def polar_groups(self, As, generators, steps=5, chain_events=None):
+        """polar_group over the tall shape groups of one optimizer step, with one
+        generator per group; returns [(polar factors, k, d)] in group order.
+
+        For the built-in arms the groups' front-ends run concurrently, each on a
+        stream of its own (they are independent, and each alone is a chain of small
+        latency-bound launches that leaves most of the GPU idle), and the chains then
+        run one after the other on the current stream.  Every group's sketch comes
+        from its own generator and every result equals that of a polar_group call.
+        chain_events: optional list of (start, end) torch.cuda.Event pairs, recorded
+        on the current stream around each group's chain."""
+        hs = self._fused(steps)
+        if hs is None or len(As) < 2 or not As[0].is_cuda:
+            # one group after the other (an arm with its own clip or iteration: the
+            # start event then marks the start of the group, not of its chain)
+            outs = []
+            for gi, (A, gen) in enumerate(zip(As, generators)):
+                ev = chain_events[gi] if chain_events else None
+                if ev is not None:
+                    ev[0].record()   # creates the HIP event; the fused call re-records it
+                outs.append(self.polar_group(A, generator=gen, steps=steps,
+                                             chain_event=ev[0] if ev is not None else None))
+                if ev is not None:
+                    ev[1].record()
+            return outs
+        dev = As[0].device
+        main = torch.cuda.current_stream(dev)
+        side = _side_streams(dev, len(As))
+        fronts = []
+        for A, gen, s in zip(As, generators, side):
+            s.wait_stream(main)
+            with torch.cuda.stream(s):
+                Bn, n, m = A.shape
+                r, kw = sketch_dims(m)
+                Omega = torch.randn(Bn, m, r, device=dev, dtype=A.dtype, generator=gen)
+                fr = _native.deflated_polar_front(A, Omega, kw, GATE_RATIO, DEFLATE_THRESH,
+                                                  self.PAD, RSVD_NITER, CHOLQR_PASSES)
+            A.record_stream(s)
+            for t in (fr.ws, fr.k, fr.d):
+                t.record_stream(main)
+            fronts.append(fr)
+        for s in side:
+            main.wait_stream(s)
+        outs = []
+        for gi, fr in enumerate(fronts):
+            ev = chain_events[gi] if chain_events else None
+            if ev is not None:
+                ev[0].record(main)
+            U = _native.deflated_polar_chain(fr, hs)
+            if ev is not None:
+                ev[1].record(main)
+            outs.append((U, fr.k, fr.d))
+        return outs
+
+
+_SIDE_STREAMS = {}
+
+
+def _side_streams(device, count):
+    """`count` streams of `device` for concurrent group front-ends (created once,
+    default priority)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    lst = _SIDE_STREAMS.setdefault(key, [])
+    while len(lst) < count:
+        lst.append(torch.cuda.Stream(device=device))
+    return lst[:count]
 
 
 class DeflatedNSPolar(_DeflatedPolarBase):

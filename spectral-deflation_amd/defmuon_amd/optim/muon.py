@@ -7,10 +7,11 @@ rate scaling and AdamW backup (muon.py:47-438).
 
 Execution differences, with identical per-matrix results: the deflated step runs
 the bf16 iteration once per tall-shape group (one grouped launch per GEMM phase
-over every matrix of the group) instead of once per parameter (muon.py:309-312),
-and for the built-in arms the clip and the iteration are one library call that
-hands X0 to the chain in its packed layout (`_DeflatedPolarBase.polar_group`).
-Each matrix's computation is independent of the others in the batch.
+over every matrix of the group) instead of once per parameter (muon.py:309-312);
+for the built-in arms the clip hands X0 to the chain in its packed layout, and
+the groups' clips run concurrently on separate streams before their chains
+(`_DeflatedPolarBase.polar_groups`).  Each matrix's computation is independent
+of the others in the batch and of the order the groups run in.
 """
 
 import math
@@ -179,21 +180,33 @@ class Muon(torch.optim.Optimizer):
             shapes.setdefault(tuple(e["A"].shape[-2:]), []).append(e)
 
         self._bd_step += 1
-        for gi, (shape, es) in enumerate(sorted(shapes.items())):
+        groups = sorted(shapes.items())
+        As, gens = [], []
+        for gi, (shape, es) in enumerate(groups):
             A = torch.cat([e["A"] for e in es], dim=0)
             gen = torch.Generator(device=A.device)
             gen.manual_seed((self._bd_step * 1009 + gi * 9176867) % (2 ** 62))
-            timed = _TIMING_ON[0] and A.is_cuda
-            if timed:
-                # separate clip and iteration calls so the events can split them
+            As.append(A)
+            gens.append(gen)
+        timed = _TIMING_ON[0] and bool(As) and As[0].is_cuda
+        if timed:
+            # one group after the other, with separate clip and iteration calls so
+            # that the events can split them
+            results, marks = [], []
+            for A, gen in zip(As, gens):
                 e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
                 e0.record()
-                X0, kvec, _ = fac.BATCHED_CLIP(A, generator=gen, pad=fac.PAD,
+                X0, kvec, d = fac.BATCHED_CLIP(A, generator=gen, pad=fac.PAD,
                                                out_dtype=torch.bfloat16)
                 e1.record()
                 Ug = fac._iterate(X0, ns_steps)      # one grouped launch per GEMM phase
-            else:
-                Ug, kvec, _ = fac.polar_group(A, generator=gen, steps=ns_steps)
+                e2.record()
+                results.append((Ug, kvec, d))
+                marks.append((e0, e1, e2))
+            _PENDING.extend(marks)
+        else:
+            results = fac.polar_groups(As, gens, steps=ns_steps)
+        for (shape, es), A, (Ug, kvec, _) in zip(groups, As, results):
             if _GATE_ACC[0] is None or _GATE_ACC[0].device != kvec.device:
                 _GATE_ACC[0] = torch.zeros(3, dtype=torch.int64, device=kvec.device)
             _GATE_ACC[0] += torch.stack([
@@ -203,9 +216,6 @@ class Muon(torch.optim.Optimizer):
             for e in es:
                 e["u"] = Ug[off:off + e["nb"]]
                 off += e["nb"]
-            if timed:
-                e2.record()
-                _PENDING.append((e0, e1, e2))
             for e in es:
                 p, g = e["p"], e["g"]
                 u = (e["u"].mT if e["tr"] else e["u"]).reshape(p.shape).bfloat16()

@@ -177,3 +177,35 @@ def test_cutoff_switches_to_plain_arm(muon_mod, monkeypatch):
     assert not opt.batched_deflation
     from defmuon_amd.optim.polar_express import PolarExpress
     assert opt.polar_factorizer is PolarExpress
+
+
+@pytest.mark.parametrize("arm", ["deflated_ns_cut", "deflated_pe_cut"])
+def test_polar_groups_equal_per_group_calls(arm):
+    """The concurrent front-ends of polar_groups (one stream per shape group, then
+    the chains in order) give bit-for-bit the per-group polar_group results:
+    polar factors, gate widths k and divisors d."""
+    from defmuon_amd import synthetic as S
+    from defmuon_amd.optim import deflation_cutoff as C
+    fac = C.ARMS[arm]()
+    shapes = [(5, 256, 256), (3, 1024, 256), (2, 520, 264)]
+    As = [torch.stack([S.spiked_matrix(n, m, seed=100 * gi + b, n_spikes=3, hi=50.0, lo=20.0)
+                       for b in range(B)]).to(DEV) for gi, (B, n, m) in enumerate(shapes)]
+
+    def gens():
+        out = []
+        for gi, A in enumerate(As):
+            g = torch.Generator(device=A.device)
+            g.manual_seed((7 * 1009 + gi * 9176867) % (2 ** 62))
+            out.append(g)
+        return out
+
+    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in As]
+    got = fac.polar_groups(As, gens(), steps=5, chain_events=evs)
+    want = [fac.polar_group(A, generator=g, steps=5) for A, g in zip(As, gens())]
+    torch.cuda.synchronize()
+    for gi, ((u1, k1, d1), (u2, k2, d2)) in enumerate(zip(got, want)):
+        assert torch.equal(k1, k2), (gi, k1, k2)
+        assert torch.equal(d1, d2), (gi, d1, d2)
+        assert torch.equal(u1.view(torch.int16), u2.view(torch.int16)), gi
+        assert k1.min().item() == 3, (gi, k1)
+        assert evs[gi][0].elapsed_time(evs[gi][1]) > 0.0
