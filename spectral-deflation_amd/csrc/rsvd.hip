@@ -29,7 +29,6 @@ constexpr int RP = 64;           // padded sketch width
 constexpr int SG_ROWS = 128;     // output rows per skinny-GEMM workgroup
 constexpr int SG_K = 32;         // K chunk
 constexpr int GRAM_CHUNKS = 8;   // row chunks of the Gram reduction
-constexpr int DT = 64;           // deflate tile (rows and columns)
 
 // ---------------------------------------------------------------------------
 // skinny GEMMs on fp32 MFMA.  v_mfma_f32_32x32x2f32: lane l supplies
@@ -1082,8 +1081,26 @@ __global__ __launch_bounds__(256) void copy_cols(const float* __restrict__ src, 
   }
 }
 
+// dst (rows x RP per matrix) = src (rows x cols, contiguous per matrix) with zero
+// columns cols..RP-1; cols = RP copies, cols = 0 zero-fills
+__global__ __launch_bounds__(256) void pad_cols(const float* __restrict__ src, int rows, int cols,
+                                                float* __restrict__ dst) {
+  const int b = blockIdx.y;
+  const long long total = (long long)rows * RP;
+  for (long long e = blockIdx.x * 256LL + threadIdx.x; e < total; e += 256LL * gridDim.x) {
+    const int row = (int)(e / RP), c = (int)(e - (long long)row * RP);
+    dst[(long long)b * total + e] =
+        c < cols ? src[((long long)b * rows + row) * cols + c] : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_zero_i32(int* __restrict__ p, int count) {
+  for (int e = blockIdx.x * 256 + threadIdx.x; e < count; e += 256 * gridDim.x) p[e] = 0;
+}
+
 // ---------------------------------------------------------------------------
-// host side
+// host side (no hipMemset/hipMemcpy: every clear and copy is a kernel, so the
+// whole sequence stays plain kernel nodes if a caller captures it in a graph)
 // ---------------------------------------------------------------------------
 struct RsvdWs {
   float *Y, *Q, *Z, *Zq, *Bt, *U, *V, *M, *Ub, *UbS, *cw, *cr, *s;
@@ -1099,6 +1116,23 @@ static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 // The split-bf16 skinny GEMMs need m and n to be multiples of 8; other shapes run the
 // fp32-MFMA kernels.
 static bool sk_fast(int n, int m) { return n % 8 == 0 && m % 8 == 0; }
+
+static int zero_ints(hipStream_t st, int* p, int count) {
+  if (count <= 0) return DMH_OK;
+  const int blocks = ceil_div(count, 256) > 1024 ? 1024 : ceil_div(count, 256);
+  hipLaunchKernelGGL(fill_zero_i32, dim3(blocks), dim3(256), 0, st, p, count);
+  DMH_CHECK_LAUNCH("fill_zero_i32");
+  return DMH_OK;
+}
+
+// dst (B, rows, RP) = src (B, rows, cols) zero-padded to RP columns
+static int pad_to_rp(hipStream_t st, const float* src, int B, int rows, int cols, float* dst) {
+  const long long total = (long long)rows * RP;
+  const int gb = ceil_div(total, 256) > 4096 ? 4096 : ceil_div(total, 256);
+  hipLaunchKernelGGL(pad_cols, dim3(gb, B), dim3(256), 0, st, src, rows, cols, dst);
+  DMH_CHECK_LAUNCH("pad_cols");
+  return DMH_OK;
+}
 
 // Row splits of sk_cols: enough waves to fill the GPU (~4096), at least 256 rows each.
 static void sk_splits(int B, int n, int m, int* S, int* rps) {
@@ -1200,8 +1234,7 @@ static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int
     src = dst;
   }
   if (passes == 0) {
-    hipMemcpyAsync(Q, Y, (size_t)B * rows * RP * sizeof(float), hipMemcpyDeviceToDevice, st);
-    DMH_CHECK_LAUNCH("orth copy");
+    if ((rc = pad_to_rp(st, Y, B, rows, RP, Q))) return rc;
     if (QT) {
       hipLaunchKernelGGL(transpose_rp, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, Y, rows, RP,
                          RP, (long long)rows * RP, QT, rows);
@@ -1248,7 +1281,7 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
                      int r, int niter, int passes, const GateParams& gp, long long* k_out,
                      float* d, const RsvdWs& w) {
   int rc;
-  hipMemsetAsync(w.degen, 0, (size_t)B * sizeof(int), st);
+  if ((rc = zero_ints(st, w.degen, B))) return rc;
   const bool fast = sk_fast(n, m);
   if (fast) {
     // split-bf16 path, 3 terms (fp32-accurate) for every product
@@ -1365,12 +1398,9 @@ int dmh_orth(hipStream_t stream, const float* X, int batch, int rows, int r, int
     return DMH_EWORKSPACE;
   }
   // pad X (rows x r) into Y (rows x RP), orthonormalise, copy out r columns
-  hipMemsetAsync(w.degen, 0, (size_t)batch * sizeof(int), stream);
-  hipMemsetAsync(w.Y, 0, (size_t)batch * rows * RP * sizeof(float), stream);
-  hipMemcpy2DAsync(w.Y, RP * sizeof(float), X, r * sizeof(float), r * sizeof(float),
-                   (size_t)batch * rows, hipMemcpyDeviceToDevice, stream);
-  DMH_CHECK_LAUNCH("dmh_orth pack");
-  int rc = orth(stream, w.Y, w.Q, w.U, batch, rows, r, passes, w);
+  int rc = zero_ints(stream, w.degen, batch);
+  if (!rc) rc = pad_to_rp(stream, X, batch, rows, r, w.Y);
+  if (!rc) rc = orth(stream, w.Y, w.Q, w.U, batch, rows, r, passes, w);
   if (rc) return rc;
   const int gb = ceil_div((long long)rows * r, 256) > 4096 ? 4096 : ceil_div((long long)rows * r, 256);
   hipLaunchKernelGGL(copy_cols, dim3(gb, batch), dim3(256), 0, stream, w.Q, rows, r, Q);
@@ -1384,8 +1414,7 @@ static int copy_usv(hipStream_t stream, const RsvdWs& w, int batch, int n, int m
   hipLaunchKernelGGL(copy_cols, dim3(gb, batch), dim3(256), 0, stream, w.U, n, r, U);
   const int gm = ceil_div((long long)m * r, 256) > 4096 ? 4096 : ceil_div((long long)m * r, 256);
   hipLaunchKernelGGL(copy_cols, dim3(gm, batch), dim3(256), 0, stream, w.V, m, r, V);
-  hipMemcpy2DAsync(s, r * sizeof(float), w.s, RP * sizeof(float), r * sizeof(float), batch,
-                   hipMemcpyDeviceToDevice, stream);
+  hipLaunchKernelGGL(copy_cols, dim3(1, batch), dim3(256), 0, stream, w.s, 1, r, s);
   DMH_CHECK_LAUNCH("U, s, V outputs");
   return DMH_OK;
 }
@@ -1403,12 +1432,10 @@ int dmh_project(hipStream_t stream, const float* Q, const float* A, int batch, i
     set_error("dmh_project: workspace %zu < %zu bytes", ws_bytes, w.bytes);
     return DMH_EWORKSPACE;
   }
-  hipMemsetAsync(w.degen, 0, (size_t)batch * sizeof(int), stream);
-  hipMemsetAsync(w.Q, 0, (size_t)batch * n * RP * sizeof(float), stream);
-  hipMemcpy2DAsync(w.Q, RP * sizeof(float), Q, r * sizeof(float), r * sizeof(float),
-                   (size_t)batch * n, hipMemcpyDeviceToDevice, stream);
-  DMH_CHECK_LAUNCH("dmh_project pack");
-  int rc = sg(stream, SG_COLSTREAM, A, batch, n, m, w.Q, RP, RP, (long long)n * RP, w.Bt,
+  int rc = zero_ints(stream, w.degen, batch);
+  if (!rc) rc = pad_to_rp(stream, Q, batch, n, r, w.Q);
+  if (rc) return rc;
+  rc = sg(stream, SG_COLSTREAM, A, batch, n, m, w.Q, RP, RP, (long long)n * RP, w.Bt,
               (long long)m * RP);
   if (rc) return rc;
   if ((rc = gram(stream, w.Bt, batch, m, w.gram))) return rc;
