@@ -41,6 +41,16 @@ WORKLOADS = {
 }
 
 
+# plain arms: the Muon parameters' matrices after the W_QKV split, nn.Linear
+# (out, in) layout, grouped as the grouped plain step launches them:
+# (count, rows, cols, tall) -- tall: the factorizer runs on the transpose
+PLAIN_GROUPS = {
+    "gpt2-small": [(48, 768, 768, False), (12, 3072, 768, True), (12, 768, 3072, False)],
+    "gpt2-medium": [(96, 1024, 1024, False), (24, 4096, 1024, True), (24, 1024, 4096, False)],
+    "gpt2-large": [(144, 1280, 1280, False), (36, 5120, 1280, True), (36, 1280, 5120, False)],
+}
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -96,6 +106,38 @@ def polar_step(fac, stacks, bd_step, ns_steps, events=None):
     return outs
 
 
+def make_plain_inputs(pgroups, device, seed=4321):
+    """Spiked-spectrum momenta per plain group, in the parameters' own layout."""
+    from defmuon_amd import synthetic as S
+    out = []
+    for gi, (B, rows, cols, tall) in enumerate(pgroups):
+        n, m = max(rows, cols), min(rows, cols)
+        X = S.spiked_batch(B, n, m, seed=seed + gi, n_spikes=8, hi=50.0, lo=10.0, device=device)
+        out.append(X if rows >= cols else X.mT.contiguous())
+    return out
+
+
+def plain_step(arm, stacks, pgroups, ns_steps, events=None):
+    """One plain-arm polar step (muon.py:361-386 factorizer calls over every Muon
+    parameter) with one launch per group, as Muon._muon_step_plain_grouped runs it."""
+    import torch
+    from defmuon_amd import _native
+    from defmuon_amd.optim.muon import NS_ABC
+    from defmuon_amd.optim.polar_express import pe_schedule
+    mode, sched = (1, [NS_ABC] * ns_steps) if arm == "ns5" else (2, pe_schedule(ns_steps))
+    evs = []
+    outs = []
+    for X, (_, _, _, tall) in zip(stacks, pgroups):
+        ev = tuple(torch.cuda.Event(enable_timing=True) for _ in range(2))
+        ev[0].record()
+        outs.append(_native.ns_chain(X, tall, mode, sched))
+        ev[1].record()
+        evs.append(ev)
+    if events is not None:
+        events.append(evs)
+    return outs
+
+
 def cpu_baseline(groups, arm, min_s=12.0, max_reps=20):
     """Time the oracle (CPU restatement of the reference arithmetic) on single
     matrices of each group -- one warm-up, then repeats until about min_s seconds
@@ -105,8 +147,9 @@ def cpu_baseline(groups, arm, min_s=12.0, max_reps=20):
     from oracle import polar_oracle as O
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    hs = O.ns_schedule(5) if arm == "deflated_ns_cut" else O.pe_schedule(5)
+    hs = O.ns_schedule(5) if arm in ("deflated_ns_cut", "ns5") else O.pe_schedule(5)
     pad = O.DIVISOR_PAD if arm == "deflated_ns_cut" else O.PE_PAD
+    plain = arm in ("ns5", "polarexpress")
     per_matrix, reps = [], []
     for gi, (B, n, m) in enumerate(groups):
         A = S.spiked_batch(1, n, m, seed=99 + gi)
@@ -115,8 +158,11 @@ def cpu_baseline(groups, arm, min_s=12.0, max_reps=20):
         times, spent = [], 0.0
         for rep in range(max_reps + 1):
             t0 = time.perf_counter()
-            X0, _, _ = O.rmfro_clip(A, Om, pad=pad, out_dtype=torch.bfloat16)
-            O.horner_iterate(X0, hs)
+            if plain:
+                (O.ns5 if arm == "ns5" else O.polar_express)(A[0], 5)
+            else:
+                X0, _, _ = O.rmfro_clip(A, Om, pad=pad, out_dtype=torch.bfloat16)
+                O.horner_iterate(X0, hs)
             dt = time.perf_counter() - t0
             if rep > 0:
                 times.append(dt)
@@ -155,7 +201,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="gpt2-large", choices=sorted(WORKLOADS))
     ap.add_argument("--arm", default="deflated_ns_cut",
-                    choices=["deflated_ns_cut", "deflated_pe_cut"])
+                    choices=["deflated_ns_cut", "deflated_pe_cut", "ns5", "polarexpress"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--inputs", default="spiked", choices=["spiked", "gaussian"],
                     help="synthetic momenta: spiked spectra (default) or i.i.d. Gaussian "
@@ -181,7 +227,8 @@ def main():
     _native.load()
     dev = torch.device("cuda", 0)
     groups = WORKLOADS[args.workload]
-    fac = C.ARMS[args.arm]()
+    plain = args.arm in ("ns5", "polarexpress")
+    fac = None if plain else C.ARMS[args.arm]()
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration * 2 ** 18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -190,13 +237,24 @@ def main():
         torch.cuda.synchronize()
         log(f"bench: copy calibration: 3 x {args.copy_calibration} MiB read + written")
         del src, dst
-    log(f"bench: generating inputs for {args.workload}: {groups}")
-    stacks = make_inputs(groups, dev, kind=args.inputs)
+    if plain:
+        pgroups = PLAIN_GROUPS[args.workload]
+        log(f"bench: generating inputs for {args.workload} ({args.arm}): {pgroups}")
+        stacks = make_plain_inputs(pgroups, dev)
+
+        def step(i, events=None):
+            return plain_step(args.arm, stacks, pgroups, 5, events)
+    else:
+        log(f"bench: generating inputs for {args.workload}: {groups}")
+        stacks = make_inputs(groups, dev, kind=args.inputs)
+
+        def step(i, events=None):
+            return polar_step(fac, stacks, i, 5, events)
     torch.cuda.synchronize()
 
     log(f"bench: warmup {args.warmup}")
     for w in range(args.warmup):
-        polar_step(fac, stacks, w + 1, 5)
+        step(w + 1)
     torch.cuda.synchronize()
     DB._GATE_ACC[0] = None
 
@@ -207,7 +265,7 @@ def main():
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
     for s in range(args.steps):
-        polar_step(fac, stacks, args.warmup + s + 1, 5, events)
+        step(args.warmup + s + 1, events)
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -215,6 +273,8 @@ def main():
     ms_per_step = gpu_ms / args.steps
     ns_ms = sum(e0.elapsed_time(e1) for evs in events for e0, e1 in evs) / args.steps
     front_ms = ms_per_step - ns_ms   # the groups' front-ends (concurrent) and the gate ticks
+    if plain:   # the chain is the whole step: same matrices, plain-arm layout
+        groups = [(B, max(r_, c_), min(r_, c_)) for B, r_, c_, _ in PLAIN_GROUPS[args.workload]]
     st = DB.polar_stats()
     flops = ns_flops(groups)
     achieved = flops / (ns_ms * 1e-3) / 1e12
@@ -261,8 +321,8 @@ def main():
                      "kernel": "NS chain (gemm_nt_bf16 K1/K2/K3 launches of a polar step), "
                                "canonical dense 4m^2n+2m^3 FLOP per matrix-iteration",
                      "flops_per_step": flops, "ns_ms_per_step": ns_ms},
-        "frontend_ms_per_step": front_ms,
-        "gate": st,
+        "frontend_ms_per_step": None if plain else front_ms,
+        "gate": None if plain else st,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -22,7 +22,7 @@ import torch
 from defmuon_amd import _native
 from defmuon_amd.optim.deflation_batched import (_DeflatedPolarBase, _GATE_ACC, _PENDING,
                                                  _TIMING_ON)
-from defmuon_amd.optim.polar_express import PolarExpress, as_batch
+from defmuon_amd.optim.polar_express import PolarExpress, as_batch, pe_schedule
 
 NS_ABC = (3.4445, -4.7750, 2.0315)
 
@@ -225,6 +225,55 @@ class Muon(torch.optim.Optimizer):
                 p.data.mul_(1 - lr * weight_decay)
                 p.data.add_(u, alpha=-adjusted_lr)
 
+    # -- the plain arms, grouped by matrix shape (grouped_plain.install()) -------
+    GROUPED_PLAIN = False
+
+    def _muon_step_plain_grouped(self, group, params, lr, weight_decay, momentum):
+        """The plain-arm update (muon.py:361-386) with one library launch per
+        (matrix shape, dtype, orientation) instead of one factorizer call per
+        parameter.  The orientation is the one the factorizer itself would pick
+        for the parameter (size(0) > size(1) for ns5, muon.py:30; size(-2) >
+        size(-1) for PolarExpress, polar_express.py:25), the entry normalisation
+        is per matrix, and the matrices of a launch do not interact, so every
+        update equals the per-parameter one.  Returns False (nothing done) for a
+        factorizer other than the built-in two."""
+        fac = self.polar_factorizer
+        steps = group["ns_steps"]
+        if fac is zeropower_via_newtonschulz5:
+            mode, sched = 1, [NS_ABC] * steps
+        elif fac is PolarExpress:
+            mode, sched = 2, pe_schedule(steps)
+        else:
+            return False
+        groups = {}
+        for p in params:
+            g = p.grad
+            if g is None:
+                continue
+            state = self.state[p]
+            if "momentum_buffer" not in state:
+                state["momentum_buffer"] = torch.zeros_like(g)
+            buf = state["momentum_buffer"]
+            buf.mul_(momentum).add_(g)
+            g = g.add(buf, alpha=momentum) if group["nesterov"] else buf
+            gq = self._qkv_split(p, g)
+            tall = gq.size(0) > gq.size(1) if mode == 1 else gq.size(-2) > gq.size(-1)
+            X = as_batch(gq)
+            groups.setdefault((tuple(X.shape[1:]), X.dtype, tall), []).append((p, g, X))
+        for (_, _, tall), es in groups.items():
+            stack = es[0][2] if len(es) == 1 else torch.cat([X for _, _, X in es])
+            out = _native.ns_chain(stack, tall, mode, sched)
+            off = 0
+            for p, g, X in es:
+                u = out[off:off + X.shape[0]].reshape(g.shape)
+                off += X.shape[0]
+                adjusted_lr = self.adjust_lr_for_muon(lr, group["rms_scaling"],
+                                                      group["nuclear_scaling"], p.shape,
+                                                      g.bfloat16(), u)
+                p.data.mul_(1 - lr * weight_decay)
+                p.data.add_(u, alpha=-adjusted_lr)
+        return True
+
     # -- step (muon.py:334-438) ------------------------------------------------
     def step(self, closure=None):
         loss = None
@@ -238,6 +287,10 @@ class Muon(torch.optim.Optimizer):
             momentum = group["momentum"]
             if self.batched_deflation and params:
                 self._muon_step_batched(group, params, lr, weight_decay, momentum)
+                params = []
+            if (self.GROUPED_PLAIN and params
+                    and self._muon_step_plain_grouped(group, params, lr, weight_decay,
+                                                      momentum)):
                 params = []
             for p in params:
                 g = p.grad

@@ -209,3 +209,33 @@ def test_polar_groups_equal_per_group_calls(arm):
         assert torch.equal(u1.view(torch.int16), u2.view(torch.int16)), gi
         assert k1.min().item() == 3, (gi, k1)
         assert evs[gi][0].elapsed_time(evs[gi][1]) > 0.0
+
+
+@pytest.mark.parametrize("arm", ["ns5", "polarexpress"])
+def test_grouped_plain_step_equals_per_parameter_loop(muon_mod, arm):
+    """grouped_plain.install(): one launch per (shape, dtype, orientation) group
+    moves every parameter bit for bit like the per-parameter loop
+    (muon.py:361-386), over two steps (momentum buffers included)."""
+    muon, DB = muon_mod
+    from defmuon_amd.optim import grouped_plain
+    results = {}
+    for grouped in (False, True):
+        if grouped:
+            grouped_plain.install()
+        else:
+            grouped_plain.uninstall()
+        try:
+            params = _named_params(7)
+            grads = _grads(params, 8)
+            opt = muon.Muon(list(params.items()), lr=0.01, weight_decay=0.1, momentum=0.95,
+                            nesterov=True, ns_steps=5, polar_method=arm)
+            for _ in range(2):
+                for k, p in params.items():
+                    p.grad = grads[k]
+                opt.step()
+            torch.cuda.synchronize()
+            results[grouped] = {k: v.detach().clone() for k, v in params.items()}
+        finally:
+            grouped_plain.uninstall()
+    for k in results[False]:
+        assert torch.equal(results[False][k], results[True][k]), k
