@@ -125,6 +125,34 @@ int dmh_deflated_polar_front(dmh_stream_t stream, const float* A, const float* O
 int dmh_deflated_polar_chain(dmh_stream_t stream, int batch, int n, int m, const double* coeffs,
                              int steps, void* out, void* ws, size_t ws_bytes);
 
+/* ---- optimizer glue either side of the polar path (one launch per group) --------
+ * One descriptor per Muon parameter of a tall-shape group.  The group's stack is
+ * (B, n, m), B = the sum of `blocks`; a parameter's block k (rows k*rows/blocks ..)
+ * is the tall matrix (n, m) = transpose ? (cols, rows/blocks) : (rows/blocks, cols),
+ * stored at stack + offset + k*n*m.  All tensors fp32 and contiguous.
+ *
+ * dmh_momentum_stack replaces muon.py:266-289 (per parameter: buf.mul_(mu).add_(g);
+ * g' = g.add(buf, alpha=mu) if nesterov else buf; _qkv_split; .float(); .mT for wide;
+ * torch.cat): momentum buffers are updated in place and g' written into `stack`.
+ * dmh_apply_update replaces muon.py:316-332 for rms scaling: p.mul_(decay) then
+ * p.add_(u, alpha) with u the bf16 polar factor read from `ustack` (same layout as
+ * the stack) and put back into the parameter's layout; alpha = -lr*sqrt(fan_out/fan_in),
+ * decay = 1 - lr*wd per parameter. */
+typedef struct {
+  const float* grad;   /* (rows, cols) */
+  float* momentum;     /* (rows, cols), updated in place */
+  float* param;        /* (rows, cols), updated in place by dmh_apply_update */
+  int rows, cols;
+  int blocks;          /* 3 for a W_QKV parameter, else 1 */
+  int transpose;       /* 1: rows/blocks < cols, the block is stored transposed */
+  long long offset;    /* elements */
+  float alpha, decay;  /* dmh_apply_update only */
+} dmh_glue_param;
+int dmh_momentum_stack(dmh_stream_t stream, const dmh_glue_param* params, int count,
+                       float momentum, int nesterov, float* stack);
+int dmh_apply_update(dmh_stream_t stream, const dmh_glue_param* params, int count,
+                     const void* ustack);
+
 #ifdef __cplusplus
 }
 #endif

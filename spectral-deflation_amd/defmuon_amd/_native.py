@@ -49,7 +49,16 @@ _SIGS = {
     "dmh_deflated_polar_chain": (c_int, [c_vp, c_int, c_int, c_int,
                                          ctypes.POINTER(ctypes.c_double), c_int, c_vp, c_vp,
                                          c_sz]),
+    "dmh_momentum_stack": (c_int, [c_vp, c_vp, c_int, c_float, c_int, c_vp]),
+    "dmh_apply_update": (c_int, [c_vp, c_vp, c_int, c_vp]),
 }
+
+
+class GlueParam(ctypes.Structure):
+    """dmh_glue_param (include/defmuon_hip.h)."""
+    _fields_ = [("grad", c_vp), ("momentum", c_vp), ("param", c_vp), ("rows", c_int),
+                ("cols", c_int), ("blocks", c_int), ("transpose", c_int),
+                ("offset", c_ll), ("alpha", c_float), ("decay", c_float)]
 
 # largest sketch width the front-end kernels carry (include/defmuon_hip.h)
 MAX_SKETCH = 64
@@ -292,3 +301,22 @@ def deflated_polar_chain(front, coeffs):
                                            _ptr(out), _ptr(front.ws), front.nbytes),
            "dmh_deflated_polar_chain")
     return out
+
+
+def momentum_stack(params, momentum, nesterov, stack):
+    """Nesterov momentum of every parameter in place and its tall fp32 blocks into
+    `stack` (B, n, m): `params` is a list of GlueParam (grad, momentum, rows, cols,
+    blocks, transpose, offset set).  Enqueued on the current stream."""
+    arr = (GlueParam * max(len(params), 1))(*params)
+    _check(load().dmh_momentum_stack(_stream(stack.device), ctypes.cast(arr, c_vp), len(params),
+                                     float(momentum), int(bool(nesterov)), _ptr(stack)),
+           "dmh_momentum_stack")
+
+
+def apply_update(params, ustack):
+    """p <- p * decay + alpha * u for every parameter, u read from the bf16 polar
+    factors `ustack` (B, n, m) in the stack layout.  Enqueued on the current stream."""
+    arr = (GlueParam * max(len(params), 1))(*params)
+    _check(load().dmh_apply_update(_stream(ustack.device), ctypes.cast(arr, c_vp), len(params),
+                                   _ptr(ustack)),
+           "dmh_apply_update")

@@ -154,9 +154,29 @@ class Muon(torch.optim.Optimizer):
         return lr * scale
 
     # -- the batched deflated step (muon.py:251-323) ---------------------------
+    # momentum -> stack and the update as one library launch per shape group
+    # (dmh_momentum_stack / dmh_apply_update); False: the reference's torch ops
+    FUSED_GLUE = True
+
+    def _fused_glue_ok(self, group, params):
+        """The fused glue covers rms scaling on contiguous fp32 GPU tensors."""
+        if not self.FUSED_GLUE or group["nuclear_scaling"]:
+            return False
+        for p in params:
+            g = p.grad
+            if g is None:
+                continue
+            buf = self.state[p].get("momentum_buffer")
+            ts = (p.data, g) if buf is None else (p.data, g, buf)
+            if any(not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous()
+                   for t in ts) or p.ndim != 2:
+                return False
+        return True
+
     def _muon_step_batched(self, group, params, lr, weight_decay, momentum):
         fac = self.polar_factorizer
         ns_steps = group["ns_steps"]
+        fused = self._fused_glue_ok(group, params)
         entries = []
         for p in params:
             if p.grad is None:
@@ -164,6 +184,14 @@ class Muon(torch.optim.Optimizer):
             state = self.state[p]
             if "momentum_buffer" not in state:
                 state["momentum_buffer"] = torch.zeros_like(p.grad)
+            if fused:
+                # the same tall blocks as below, described instead of materialised
+                rows, cols = p.shape
+                nb = 3 if state.get("is_W_QKV", False) else 1
+                tr = rows // nb < cols
+                shape = (cols, rows // nb) if tr else (rows // nb, cols)
+                entries.append({"p": p, "tr": tr, "nb": nb, "shape": shape})
+                continue
             buf = state["momentum_buffer"]
             buf.mul_(momentum).add_(p.grad)
             g = p.grad.add(buf, alpha=momentum) if group["nesterov"] else buf
@@ -173,17 +201,24 @@ class Muon(torch.optim.Optimizer):
             tr = A.shape[-2] < A.shape[-1]
             if tr:
                 A = A.mT
-            entries.append({"p": p, "g": g, "A": A, "tr": tr, "nb": A.shape[0]})
+            entries.append({"p": p, "g": g, "A": A, "tr": tr, "nb": A.shape[0],
+                            "shape": tuple(A.shape[-2:])})
 
         shapes = {}
         for e in entries:
-            shapes.setdefault(tuple(e["A"].shape[-2:]), []).append(e)
+            shapes.setdefault(e["shape"], []).append(e)
 
         self._bd_step += 1
         groups = sorted(shapes.items())
         As, gens = [], []
         for gi, (shape, es) in enumerate(groups):
-            A = torch.cat([e["A"] for e in es], dim=0)
+            if fused:
+                A = torch.empty((sum(e["nb"] for e in es),) + shape, dtype=torch.float32,
+                                device=es[0]["p"].device)
+                _native.momentum_stack(self._glue_params(es, shape), momentum,
+                                       group["nesterov"], A)
+            else:
+                A = torch.cat([e["A"] for e in es], dim=0)
             gen = torch.Generator(device=A.device)
             gen.manual_seed((self._bd_step * 1009 + gi * 9176867) % (2 ** 62))
             As.append(A)
@@ -212,6 +247,9 @@ class Muon(torch.optim.Optimizer):
             _GATE_ACC[0] += torch.stack([
                 torch.tensor(A.shape[0], dtype=torch.int64, device=kvec.device),
                 (kvec > 0).sum(), kvec.sum().to(torch.int64)])
+            if fused:
+                _native.apply_update(self._glue_params(es, shape, lr, weight_decay, group), Ug)
+                continue
             off = 0
             for e in es:
                 e["u"] = Ug[off:off + e["nb"]]
@@ -224,6 +262,30 @@ class Muon(torch.optim.Optimizer):
                                                       g.bfloat16(), u)
                 p.data.mul_(1 - lr * weight_decay)
                 p.data.add_(u, alpha=-adjusted_lr)
+
+    def _glue_params(self, es, shape, lr=None, weight_decay=0.0, group=None):
+        """dmh_glue_param descriptors of a shape group's parameters, in stack order;
+        with lr, the update's alpha = -lr * sqrt(fan_out / fan_in) (rms scaling, as
+        adjust_lr_for_muon) and decay = 1 - lr * wd."""
+        n, m = shape
+        out, off = [], 0
+        for e in es:
+            p = e["p"]
+            d = _native.GlueParam()
+            d.grad = p.grad.data_ptr()
+            d.momentum = self.state[p]["momentum_buffer"].data_ptr()
+            d.param = p.data.data_ptr()
+            d.rows, d.cols = p.shape
+            d.blocks = e["nb"]
+            d.transpose = int(e["tr"])
+            d.offset = off * n * m
+            if lr is not None:
+                d.alpha = -self.adjust_lr_for_muon(lr, group["rms_scaling"], False, p.shape,
+                                                   None, None)
+                d.decay = 1 - lr * weight_decay
+            off += e["nb"]
+            out.append(d)
+        return out
 
     # -- the plain arms, grouped by matrix shape (grouped_plain.install()) -------
     GROUPED_PLAIN = False

@@ -239,3 +239,33 @@ def test_grouped_plain_step_equals_per_parameter_loop(muon_mod, arm):
             grouped_plain.uninstall()
     for k in results[False]:
         assert torch.equal(results[False][k], results[True][k]), k
+
+
+@pytest.mark.parametrize("nesterov", [True, False])
+def test_fused_glue_equals_torch_ops(muon_mod, nesterov):
+    """dmh_momentum_stack / dmh_apply_update (one launch per shape group) leave
+    every parameter and momentum buffer bit for bit where the reference's torch
+    ops (muon.py:266-289, 316-332) do, over two deflated steps: W_QKV blocks,
+    square, tall and wide (transposed) parameters, weight decay."""
+    muon, DB = muon_mod
+    results = {}
+    for fused in (False, True):
+        params = _named_params(9)
+        grads = _grads(params, 10)
+        opt = muon.Muon(list(params.items()), lr=0.02, weight_decay=0.1, momentum=0.9,
+                        nesterov=nesterov, ns_steps=5, polar_method="deflated_ns_cut")
+        opt.FUSED_GLUE = fused
+        for step in range(2):
+            for k, p in params.items():
+                p.grad = grads[k] * (1.0 + 0.5 * step)
+            opt.step()
+        torch.cuda.synchronize()
+        bufs = {k: opt.state[p]["momentum_buffer"].clone() for k, p in params.items()
+                if "momentum_buffer" in opt.state[p]}
+        results[fused] = ({k: v.detach().clone() for k, v in params.items()}, bufs)
+    (p0, b0), (p1, b1) = results[False], results[True]
+    assert b0.keys() == b1.keys() and len(b0) == 4 * LAYERS
+    for k in b0:
+        assert torch.equal(b0[k], b1[k]), ("momentum", k)
+    for k in p0:
+        assert torch.equal(p0[k], p1[k]), ("param", k, (p0[k] - p1[k]).abs().max().item())
