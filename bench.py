@@ -138,6 +138,138 @@ def plain_step(arm, stacks, pgroups, ns_steps, events=None):
     return outs
 
 
+def _gpt2(vocab, ctx, d, layers, heads):
+    """GPT-2 with nn.Linear weights named as the reference's model names them
+    (attn.c_attn, attn.c_proj, mlp.c_fc, mlp.c_proj; wte, wpe, tied lm_head), so
+    Muon routes and splits them the same way; bf16 autocast in the forward."""
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    class Attn(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.c_attn, self.c_proj = nn.Linear(d, 3 * d), nn.Linear(d, d)
+
+        def forward(self, x):
+            B, T, _ = x.shape
+            q, k, v = (t.view(B, T, heads, d // heads).transpose(1, 2)
+                       for t in self.c_attn(x).split(d, dim=2))
+            y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            return self.c_proj(y.transpose(1, 2).reshape(B, T, d))
+
+    class Mlp(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.c_fc, self.c_proj = nn.Linear(d, 4 * d), nn.Linear(4 * d, d)
+
+        def forward(self, x):
+            return self.c_proj(F.gelu(self.c_fc(x), approximate="tanh"))
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ln_1, self.attn, self.ln_2, self.mlp = nn.LayerNorm(d), Attn(), nn.LayerNorm(d), Mlp()
+
+        def forward(self, x):
+            x = x + self.attn(self.ln_1(x))
+            return x + self.mlp(self.ln_2(x))
+
+    class GPT(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.wte, self.wpe = nn.Embedding(vocab, d), nn.Embedding(ctx, d)
+            self.h = nn.ModuleList(Block() for _ in range(layers))
+            self.ln_f = nn.LayerNorm(d)
+            self.lm_head = nn.Linear(d, vocab, bias=False)
+            self.lm_head.weight = self.wte.weight
+
+        def forward(self, idx, targets):
+            x = self.wte(idx) + self.wpe(torch.arange(idx.shape[1], device=idx.device))
+            for blk in self.h:
+                x = blk(x)
+            logits = self.lm_head(self.ln_f(x))
+            return F.cross_entropy(logits.float().view(-1, vocab), targets.reshape(-1))
+
+    return GPT()
+
+
+def train_step_report(args, dev):
+    """Config 5: a GPT-2-large training step (batch 8 x 1024 random tokens, random
+    init), Muon deflated_ns_cut on the 144 hidden matrices (216 after the W_QKV
+    split), AdamW on embeddings, norms and biases.  Reports the step time, its
+    forward+backward and optimizer parts, the polar path inside the optimizer step
+    (events around the groups' clips + iterations) and its share, and the optimizer
+    step with the reference's torch glue instead of the fused glue."""
+    import torch
+    from defmuon_amd.optim import deflation_cutoff
+    from defmuon_amd.optim.muon import Muon
+    deflation_cutoff.install()
+    torch.manual_seed(0)
+    model = _gpt2(50257, 1024, 1280, 36, 20).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    tok = torch.randint(0, 50257, (8, 1025), device=dev, generator=g)
+    x, y = tok[:, :-1], tok[:, 1:]
+    opt = Muon(model.named_parameters(), lr=0.01, weight_decay=0.0, momentum=0.95, nesterov=True,
+               ns_steps=5, polar_method="deflated_ns_cut")
+    fac = opt.polar_factorizer
+    orig = fac.polar_groups
+    marks = []
+
+    def timed_groups(As, gens, steps=5, chain_events=None):
+        e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        e[0].record()
+        out = orig(As, gens, steps=steps, chain_events=chain_events)
+        e[1].record()
+        marks.append(e)
+        return out
+    fac.polar_groups = timed_groups
+
+    def one(evs):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = model(x, y)
+        loss.backward()
+        e[1].record()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        e[2].record()
+        evs.append(e)
+
+    res = {}
+    for fused in (True, False):
+        opt.FUSED_GLUE = fused
+        for _ in range(args.warmup):
+            one([])
+        torch.cuda.synchronize()
+        marks.clear()
+        evs = []
+        for _ in range(args.steps):
+            one(evs)
+        torch.cuda.synchronize()
+        step = sum(e[0].elapsed_time(e[2]) for e in evs) / args.steps
+        fb = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+        optm = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+        polar = sum(m[0].elapsed_time(m[1]) for m in marks) / args.steps
+        res[fused] = dict(step_ms=step, fwd_bwd_ms=fb, optimizer_ms=optm, polar_ms=polar)
+        log(f"bench train: fused glue {fused}: {res[fused]}")
+    f = res[True]
+    return {"metric": "GPT-2-large training step (config 5): polar-factor share of step time",
+            "value": f["polar_ms"] / f["step_ms"], "unit": "fraction of step time",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": f["step_ms"], "higher_is_better": False,
+            "tokens_per_s": 8 * 1024 / (f["step_ms"] * 1e-3),
+            "fwd_bwd_ms": f["fwd_bwd_ms"], "optimizer_ms": f["optimizer_ms"],
+            "polar_ms": f["polar_ms"], "optimizer_ms_torch_glue": res[False]["optimizer_ms"],
+            "dtype": "bf16 autocast (model), bf16/fp32/fp64 (polar path)",
+            "data": "random init, random token ids uniform over 50257, batch 8 x 1024",
+            "config": {"workload": "gpt2-large train step: d=1280, 36 layers, 20 heads, MLP "
+                                   "5120; Muon deflated_ns_cut on 144 hidden matrices, AdamW "
+                                   "on the rest"}}
+
+
 def cpu_baseline(groups, arm, min_s=12.0, max_reps=20):
     """Time the oracle (CPU restatement of the reference arithmetic) on single
     matrices of each group -- one warm-up, then repeats until about min_s seconds
@@ -206,6 +338,9 @@ def main():
     ap.add_argument("--inputs", default="spiked", choices=["spiked", "gaussian"],
                     help="synthetic momenta: spiked spectra (default) or i.i.d. Gaussian "
                          "(for counter runs; no solver call)")
+    ap.add_argument("--mode", default="polar", choices=["polar", "train"],
+                    help="polar: the polar-step bench (default); train: the GPT-2-large "
+                         "training step of config 5, with the polar-factor share")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="before the steps, copy a MIB-MiB fp32 buffer three times with "
                          "torch's copy kernel: a known-size reference for HBM byte "
@@ -226,6 +361,9 @@ def main():
         sys.exit(1)
     _native.load()
     dev = torch.device("cuda", 0)
+    if args.mode == "train":
+        print(json.dumps(train_step_report(args, dev)), flush=True)
+        return
     groups = WORKLOADS[args.workload]
     plain = args.arm in ("ns5", "polarexpress")
     fac = None if plain else C.ARMS[args.arm]()
