@@ -220,8 +220,11 @@ class _DeflatedPolarBase:
         dev = As[0].device
         main = torch.cuda.current_stream(dev)
         side = _side_streams(dev, len(As))
-        fronts = []
-        for A, gen, s in zip(As, generators, side):
+        # the largest front-end (the critical path) is enqueued first
+        order = sorted(range(len(As)), key=lambda gi: -As[gi].numel())
+        fronts = [None] * len(As)
+        for s, gi in zip(side, order):
+            A, gen = As[gi], generators[gi]
             s.wait_stream(main)
             with torch.cuda.stream(s):
                 Bn, n, m = A.shape
@@ -232,7 +235,7 @@ class _DeflatedPolarBase:
             A.record_stream(s)
             for t in (fr.ws, fr.k, fr.d):
                 t.record_stream(main)
-            fronts.append(fr)
+            fronts[gi] = fr
         for s in side:
             main.wait_stream(s)
         outs = []
