@@ -117,7 +117,8 @@ int dmh_deflated_polar(dmh_stream_t stream, const float* A, const float* Omega, 
  *           chain's packed operand inside ws; writes k and d.
  *   _chain: the bf16 iteration (deflation_batched.py:196-211 via muon.py:310-312)
  *           from that operand, same batch/n/m, to out (batch, n, m) bf16.
- * ws must stay untouched between the two calls (stream-ordered). */
+ * ws must stay untouched between the two calls (stream-ordered); the chain works in
+ * place on the entry, so each _front is followed by one chain call. */
 int dmh_deflated_polar_front(dmh_stream_t stream, const float* A, const float* Omega, int batch,
                              int n, int m, int r, int kw, float ratio, float thresh, float pad,
                              int niter, int qr_passes, long long* k, float* d, void* ws,

@@ -1136,7 +1136,7 @@ static int pad_to_rp(hipStream_t st, const float* src, int B, int rows, int cols
 
 // Row splits of sk_cols: enough waves to fill the GPU (~4096), at least 256 rows each.
 static void sk_splits(int B, int n, int m, int* S, int* rps) {
-  const long long waves = (long long)ceil_div(m, SKC_COLS) * B;
+  const long long waves = (long long)ceil_div(m, SKC_COLS) * (B > 0 ? B : 1);
   int s = (int)((4096 + waves - 1) / waves);
   s = s < 1 ? 1 : (s > SK_MAXS ? SK_MAXS : s);
   while (s > 1 && n / s < 256) --s;

@@ -65,3 +65,12 @@ def test_entry_points_reject_bad_arguments_without_launching(lib):
     assert b"workspace" in lib.dmh_last_error()
     # batch 0 is a no-op
     assert lib.dmh_orth(v, None, 0, 10, 2, 1, None, None, 0) == 0
+
+
+def test_workspace_sizes_for_empty_batch(lib):
+    """An empty shape group (batch 0) sizes its workspaces without faulting."""
+    n = ctypes.c_size_t()
+    for fn in ("dmh_rsvd_workspace_size", "dmh_rmfro_workspace_size",
+               "dmh_deflated_polar_workspace_size"):
+        assert getattr(lib, fn)(0, 512, 256, 14, ctypes.byref(n)) == 0, fn
+    assert lib.dmh_ns_workspace_size(0, 512, 256, 1, ctypes.byref(n)) == 0
