@@ -401,15 +401,90 @@ __device__ __forceinline__ f32x16 mfma_split(const bf16x8 (&a)[SPLITS], const bf
 }
 
 constexpr int SKR_ROWS = 256;   // rows of A per sk_rows workgroup (4 waves x 64)
-constexpr int SKC_COLS = 64;    // columns of A per sk_cols wave
+constexpr int SKC_COLS = 256;   // columns of A per sk_cols workgroup (4 waves x 64)
+constexpr int SKC_TARGET = 1024;   // sk_cols workgroups to aim for (row splits)
 constexpr int SK_MAXS = 16;     // maximum row splits of sk_cols
+
+// The small operand S of a skinny product (RP x lds fp32, row c = its column c) is the
+// first MFMA operand: lane l supplies row 32 cb + l % 32 and 8 contraction indices.  A
+// workgroup stages chunks of SK_KC contraction indices of S in LDS, already split into
+// bf16 terms, so each chunk is read from L2 and split once per workgroup rather than
+// once per wave; the waves then read their fragments from LDS.  Rows are padded to
+// SK_PITCH bf16 (144 B), which makes the 16-byte fragment reads of 16 consecutive lanes
+// cover the 64 banks once.  Two chunk buffers: the next chunk is written while the
+// current one is read, one barrier per chunk.
+constexpr int SK_KC = 64;
+constexpr int SK_PITCH = SK_KC + 8;
+constexpr int SK_TERM = RP * SK_PITCH;       // bf16 per split term
+constexpr int SK_BUF = 3 * SK_TERM;          // bf16 per chunk buffer (up to 3 terms)
+
+// Thread t stages the units u = t and t + 256 of a chunk: row c = u / 8, contraction
+// indices k0 + 8 (u % 8) .. +7 (zero at and beyond kend; 8-index groups are whole).
+struct SkStage {
+  float4 v[2][2];
+};
+
+__device__ __forceinline__ void sk_stage_load(SkStage& st, const float* __restrict__ S, int lds,
+                                              int k0, int kend, int tid) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int u = tid + 256 * q;
+    const int c = u >> 3, k = k0 + 8 * (u & 7);
+    const bool ok = k < kend;
+    const float* p = S + (long long)c * lds + (ok ? k : 0);
+    st.v[q][0] = ok ? *(const float4*)p : make_float4(0.f, 0.f, 0.f, 0.f);
+    st.v[q][1] = ok ? *(const float4*)(p + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+template <int SPLITS>
+__device__ __forceinline__ void sk_stage_store(const SkStage& st, bf16* buf, int tid) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int u = tid + 256 * q;
+    const int c = u >> 3, kk = 8 * (u & 7);
+    const float x[8] = {st.v[q][0].x, st.v[q][0].y, st.v[q][0].z, st.v[q][0].w,
+                        st.v[q][1].x, st.v[q][1].y, st.v[q][1].z, st.v[q][1].w};
+    bf16x8 t[SPLITS];
+    split_bf16<SPLITS>(x, t);
+#pragma unroll
+    for (int s = 0; s < SPLITS; ++s) *(bf16x8*)(buf + s * SK_TERM + c * SK_PITCH + kk) = t[s];
+  }
+}
+
+// Fragments of the staged chunk for contraction offset koff (within the chunk) of
+// this lane: rows 32 cb + l32, indices koff .. koff + 7.
+template <int SPLITS>
+__device__ __forceinline__ void sk_frags(const bf16* buf, int koff, int l32,
+                                         bf16x8 (&xs)[2][SPLITS]) {
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int s = 0; s < SPLITS; ++s)
+      xs[cb][s] = *(const bf16x8*)(buf + s * SK_TERM + (32 * cb + l32) * SK_PITCH + koff);
+}
+
+// Workgroup barrier for the chunk buffers: the LDS writes and reads issued before it
+// have completed (lgkmcnt), global loads in flight stay in flight.  The empty asm
+// statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void sk_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // C (n x RP, per matrix) = A (n x m) X, with X given transposed: XT (RP x ldxt),
 // XT[c][k] = X[k][c].  Needs m % 8 == 0.  asq: per-workgroup sums of squares of A.
+// Wave w owns rows r0 .. r0 + 63 (two 32-row MFMA blocks).  A is read 32 contraction
+// indices at a time: lane (l32, h) loads 16 consecutive floats of its two rows at
+// 32 j + 16 h, so each 128-byte line of A is requested by one instruction group; the
+// two k16 MFMA substeps of the step take the lane's floats 0-7 and 8-15 (contraction
+// order is free as long as the staged X fragments follow the same indices).
 template <int SPLITS>
 __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int n, int m,
                                                const float* __restrict__ XT, int ldxt,
                                                float* __restrict__ C, double* __restrict__ asq) {
+  __shared__ __attribute__((aligned(16))) bf16 xl[2 * SK_BUF];
   const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hk = lane >> 5;
   const int r0 = blockIdx.x * SKR_ROWS + wave * 64;
@@ -422,11 +497,8 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
   for (int rb = 0; rb < 2; ++rb) {
     const int i = r0 + 32 * rb + l32;
     ain[rb] = i < n;
-    ap[rb] = A + (long long)(ain[rb] ? i : 0) * m + 8 * hk;
+    ap[rb] = A + (long long)(ain[rb] ? i : 0) * m + 16 * hk;
   }
-  const float* xp[2];
-#pragma unroll
-  for (int cb = 0; cb < 2; ++cb) xp[cb] = XT + (long long)(32 * cb + l32) * ldxt + 8 * hk;
   f32x16 acc[2][2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
@@ -435,54 +507,67 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[rb][cb][e] = 0.f;
   double sq = 0.0;
-  const int nk = (m + 15) / 16;
-  float4 an[2][2], xn[2][2];
-  auto load = [&](int ks, float4 (&a)[2][2], float4 (&x)[2][2]) {
-    const int k = 16 * ks;
-    const bool kin = k + 8 * hk < m;
+  const int nk = (m + 31) / 32;             // 32-index steps
+  const int nch = (m + SK_KC - 1) / SK_KC;  // staged chunks
+  // floats 8 q .. 8 q + 7 of the lane's 16 at step ks: indices 32 ks + 16 hk + 8 q ..
+  auto load = [&](int ks, float4 (&a)[2][4]) {
+    const int k = 32 * ks;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const bool ok = kin && ain[rb];
-      a[rb][0] = ok ? *(const float4*)(ap[rb] + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-      a[rb][1] = ok ? *(const float4*)(ap[rb] + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int v = 0; v < 4; ++v) {
+      const bool kin = k + 16 * hk + 4 * v < m;   // m % 8 == 0: 8-index groups are whole
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      x[cb][0] = kin ? *(const float4*)(xp[cb] + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-      x[cb][1] = kin ? *(const float4*)(xp[cb] + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int rb = 0; rb < 2; ++rb)
+        a[rb][v] = (kin && ain[rb]) ? *(const float4*)(ap[rb] + k + 4 * v)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  load(0, an, xn);
-  for (int ks = 0; ks < nk; ++ks) {
-    float4 ac[2][2], xc[2][2];
+  SkStage stg;
+  sk_stage_load(stg, XT, ldxt, 0, m, tid);
+  sk_stage_store<SPLITS>(stg, xl, tid);
+  if (nch > 1) sk_stage_load(stg, XT, ldxt, SK_KC, m, tid);
+  float4 an[2][4];
+  load(0, an);
+  sk_barrier();
+  for (int ch = 0; ch < nch; ++ch) {
+    const bf16* buf = xl + (ch & 1) * SK_BUF;
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int p = 0; p < SK_KC / 32; ++p) {
+      const int ks = ch * (SK_KC / 32) + p;
+      if (ks >= nk) break;
+      float4 ac[2][4];
 #pragma unroll
-      for (int v = 0; v < 2; ++v) { ac[u][v] = an[u][v]; xc[u][v] = xn[u][v]; }
-    if (ks + 1 < nk) load(ks + 1, an, xn);
-    bf16x8 as[2][SPLITS], xs[2][SPLITS];
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const float v[8] = {ac[rb][0].x, ac[rb][0].y, ac[rb][0].z, ac[rb][0].w,
-                          ac[rb][1].x, ac[rb][1].y, ac[rb][1].z, ac[rb][1].w};
-      if (asq) {
-        float f = 0.f;
+        for (int v = 0; v < 4; ++v) ac[rb][v] = an[rb][v];
+      if (ks + 1 < nk) load(ks + 1, an);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f = fmaf(v[e], v[e], f);
-        sq += (double)f;
+      for (int q = 0; q < 2; ++q) {
+        bf16x8 as[2][SPLITS], xs[2][SPLITS];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          const float4 lo = ac[rb][2 * q], hi = ac[rb][2 * q + 1];
+          const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+          if (asq) {
+            float f = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f = fmaf(v[e], v[e], f);
+            sq += (double)f;
+          }
+          split_bf16<SPLITS>(v, as[rb]);
+        }
+        sk_frags<SPLITS>(buf, 32 * p + 16 * hk + 8 * q, l32, xs);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            acc[rb][cb] = mfma_split<SPLITS>(xs[cb], as[rb], acc[rb][cb]);
       }
-      split_bf16<SPLITS>(v, as[rb]);
     }
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const float v[8] = {xc[cb][0].x, xc[cb][0].y, xc[cb][0].z, xc[cb][0].w,
-                          xc[cb][1].x, xc[cb][1].y, xc[cb][1].z, xc[cb][1].w};
-      split_bf16<SPLITS>(v, xs[cb]);
+    if (ch + 1 < nch) {
+      sk_stage_store<SPLITS>(stg, xl + ((ch + 1) & 1) * SK_BUF, tid);
+      sk_barrier();
+      if (ch + 2 < nch) sk_stage_load(stg, XT, ldxt, (ch + 2) * SK_KC, m, tid);
     }
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = mfma_split<SPLITS>(xs[cb], as[rb], acc[rb][cb]);
   }
   // D[c][i] = C[i][c]: lane holds rows c = 32 cb + 8 g + 4 hk + q of column i = l32
 #pragma unroll
@@ -511,17 +596,20 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
 
 // Partial C = A^T Y over the rows [s * rps, (s+1) * rps) of split s = blockIdx.y:
 // part[s][b] (m x RP) = sum_i A[i][j] Y[i][c], with Y given transposed: YT (RP x
-// ldyt), YT[c][i] = Y[i][c].  One wave per 64 columns of A; lane l reads the
-// columns j0 + 2 l32 + {0, 1} of 8 consecutive rows, i.e. two 32-column MFMA
-// blocks (block e holds the columns j0 + 2 l32 + e).  Needs m % 2 == 0, n % 8 == 0.
+// ldyt), YT[c][i] = Y[i][c] (staged in LDS like sk_rows' X).  Wave w owns 64 columns
+// of A; lane l reads the columns j0 + 2 l32 + {0, 1} of 8 consecutive rows, i.e. two
+// 32-column MFMA blocks (block e holds the columns j0 + 2 l32 + e).  Needs m % 2 == 0,
+// n % 8 == 0 and rps % 16 == 0.
 template <int SPLITS>
-__global__ __launch_bounds__(64) void sk_cols(const float* __restrict__ A, int n, int m,
-                                              const float* __restrict__ YT, int ldyt, int rps,
-                                              float* __restrict__ part) {
-  const int b = blockIdx.z, s = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void sk_cols(const float* __restrict__ A, int n, int m,
+                                               const float* __restrict__ YT, int ldyt, int rps,
+                                               float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) bf16 yl[2 * SK_BUF];
+  const int b = blockIdx.z, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63,
+            wave = tid >> 6;
   const int l32 = lane & 31, hk = lane >> 5;
   const int nb = gridDim.z;
-  const int j0 = blockIdx.x * SKC_COLS;
+  const int j0 = blockIdx.x * SKC_COLS + 64 * wave;
   const int jl = j0 + 2 * l32;           // this lane's two columns
   const bool jin = jl < m;
   A += (long long)b * n * m;
@@ -534,51 +622,51 @@ __global__ __launch_bounds__(64) void sk_cols(const float* __restrict__ A, int n
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[e][cb][v] = 0.f;
-  const float* yp[2];
-#pragma unroll
-  for (int cb = 0; cb < 2; ++cb) yp[cb] = YT + (long long)(32 * cb + l32) * ldyt;
   const int nk = (ie - ib + 15) / 16;
-  float2 an[8];
-  float4 yn[2][2];
-  auto load = [&](int ks, float2 (&a)[8], float4 (&y)[2][2]) {
+  const int nch = (ie - ib + SK_KC - 1) / SK_KC;
+  auto load = [&](int ks, float2 (&a)[8]) {
     const int i0 = ib + 16 * ks + 8 * hk;
-    const bool iin = i0 < ie;            // n % 8 == 0: 8-row chunks are whole
+    const bool iin = i0 < ie;            // 8-row groups are whole
 #pragma unroll
     for (int t = 0; t < 8; ++t)
       a[t] = (iin && jin) ? *(const float2*)(A + (long long)(i0 + t) * m + jl)
                           : make_float2(0.f, 0.f);
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      y[cb][0] = iin ? *(const float4*)(yp[cb] + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
-      y[cb][1] = iin ? *(const float4*)(yp[cb] + i0 + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
   };
-  load(0, an, yn);
-  for (int ks = 0; ks < nk; ++ks) {
-    float2 ac[8];
-    float4 yc[2][2];
+  SkStage stg;
+  sk_stage_load(stg, YT, ldyt, ib, ie, tid);
+  sk_stage_store<SPLITS>(stg, yl, tid);
+  if (nch > 1) sk_stage_load(stg, YT, ldyt, ib + SK_KC, ie, tid);
+  float2 an[8];
+  load(0, an);
+  sk_barrier();
+  for (int ch = 0; ch < nch; ++ch) {
+    const bf16* buf = yl + (ch & 1) * SK_BUF;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) ac[t] = an[t];
+    for (int p = 0; p < SK_KC / 16; ++p) {
+      const int ks = ch * (SK_KC / 16) + p;
+      if (ks >= nk) break;
+      float2 ac[8];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) { yc[cb][0] = yn[cb][0]; yc[cb][1] = yn[cb][1]; }
-    if (ks + 1 < nk) load(ks + 1, an, yn);
-    bf16x8 as[2][SPLITS], ys[2][SPLITS];
-    {
-      const float v0[8] = {ac[0].x, ac[1].x, ac[2].x, ac[3].x, ac[4].x, ac[5].x, ac[6].x, ac[7].x};
-      const float v1[8] = {ac[0].y, ac[1].y, ac[2].y, ac[3].y, ac[4].y, ac[5].y, ac[6].y, ac[7].y};
-      split_bf16<SPLITS>(v0, as[0]);
-      split_bf16<SPLITS>(v1, as[1]);
+      for (int t = 0; t < 8; ++t) ac[t] = an[t];
+      if (ks + 1 < nk) load(ks + 1, an);
+      bf16x8 as[2][SPLITS], ys[2][SPLITS];
+      {
+        const float v0[8] = {ac[0].x, ac[1].x, ac[2].x, ac[3].x, ac[4].x, ac[5].x, ac[6].x, ac[7].x};
+        const float v1[8] = {ac[0].y, ac[1].y, ac[2].y, ac[3].y, ac[4].y, ac[5].y, ac[6].y, ac[7].y};
+        split_bf16<SPLITS>(v0, as[0]);
+        split_bf16<SPLITS>(v1, as[1]);
+      }
+      sk_frags<SPLITS>(buf, 16 * p + 8 * hk, l32, ys);
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) acc[e][cb] = mfma_split<SPLITS>(ys[cb], as[e], acc[e][cb]);
     }
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const float v[8] = {yc[cb][0].x, yc[cb][0].y, yc[cb][0].z, yc[cb][0].w,
-                          yc[cb][1].x, yc[cb][1].y, yc[cb][1].z, yc[cb][1].w};
-      split_bf16<SPLITS>(v, ys[cb]);
+    if (ch + 1 < nch) {
+      sk_stage_store<SPLITS>(stg, yl + ((ch + 1) & 1) * SK_BUF, tid);
+      sk_barrier();
+      if (ch + 2 < nch) sk_stage_load(stg, YT, ldyt, ib + (ch + 2) * SK_KC, ie, tid);
     }
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) acc[e][cb] = mfma_split<SPLITS>(ys[cb], as[e], acc[e][cb]);
   }
   // D[c][col] = C[j][c], col = l32 -> j = j0 + 2 l32 + e
   float* pb = part + ((long long)s * nb + b) * m * RP;
@@ -1134,10 +1222,10 @@ static int pad_to_rp(hipStream_t st, const float* src, int B, int rows, int cols
   return DMH_OK;
 }
 
-// Row splits of sk_cols: enough waves to fill the GPU (~4096), at least 256 rows each.
+// Row splits of sk_cols: about SKC_TARGET workgroups in all, at least 256 rows each.
 static void sk_splits(int B, int n, int m, int* S, int* rps) {
-  const long long waves = (long long)ceil_div(m, SKC_COLS) * (B > 0 ? B : 1);
-  int s = (int)((4096 + waves - 1) / waves);
+  const long long wgs = (long long)ceil_div(m, SKC_COLS) * (B > 0 ? B : 1);
+  int s = (int)((SKC_TARGET + wgs - 1) / wgs);
   s = s < 1 ? 1 : (s > SK_MAXS ? SK_MAXS : s);
   while (s > 1 && n / s < 256) --s;
   int r = ceil_div(n, s);
@@ -1245,28 +1333,22 @@ static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int
 }
 
 // Y (n x RP) = A XT^T with the split-bf16 kernel (XT: RP x m); asq optional
-static int skr(hipStream_t st, int splits, const float* A, int B, int n, int m, const float* XT,
-               float* Y, double* asq) {
+static int skr(hipStream_t st, const float* A, int B, int n, int m, const float* XT, float* Y,
+               double* asq) {
   dim3 grid(ceil_div(n, SKR_ROWS), B);
-  if (splits == 3)
-    hipLaunchKernelGGL(sk_rows<3>, grid, dim3(256), 0, st, A, n, m, XT, m, Y, asq);
-  else
-    hipLaunchKernelGGL(sk_rows<2>, grid, dim3(256), 0, st, A, n, m, XT, m, Y, asq);
+  hipLaunchKernelGGL(sk_rows<3>, grid, dim3(256), 0, st, A, n, m, XT, m, Y, asq);
   DMH_CHECK_LAUNCH("sk_rows");
   return DMH_OK;
 }
 
 // C (m x RP) = A^T YT^T with the split-bf16 kernel (YT: RP x n), row splits reduced
 // in order
-static int skc(hipStream_t st, int splits, const float* A, int B, int n, int m, const float* YT,
-               float* C, const RsvdWs& w) {
+static int skc(hipStream_t st, const float* A, int B, int n, int m, const float* YT, float* C,
+               const RsvdWs& w) {
   int S, rps;
   sk_splits(B, n, m, &S, &rps);
   dim3 grid(ceil_div(m, SKC_COLS), S, B);
-  if (splits == 3)
-    hipLaunchKernelGGL(sk_cols<3>, grid, dim3(64), 0, st, A, n, m, YT, n, rps, w.part);
-  else
-    hipLaunchKernelGGL(sk_cols<2>, grid, dim3(64), 0, st, A, n, m, YT, n, rps, w.part);
+  hipLaunchKernelGGL(sk_cols<3>, grid, dim3(256), 0, st, A, n, m, YT, n, rps, w.part);
   DMH_CHECK_LAUNCH("sk_cols");
   const long long per = (long long)B * m * RP;
   hipLaunchKernelGGL(sk_reduce, dim3((unsigned)ceil_div(per / 4, 256)), dim3(256), 0, st, w.part,
@@ -1288,15 +1370,15 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
     hipLaunchKernelGGL(transpose_rp, dim3(ceil_div(m, 64), B), dim3(256), 0, st, Omega, m, r, r,
                        (long long)m * r, w.XT, m);
     DMH_CHECK_LAUNCH("transpose Omega");
-    if ((rc = skr(st, 3, A, B, n, m, w.XT, w.Y, d ? w.asq : nullptr))) return rc;
+    if ((rc = skr(st, A, B, n, m, w.XT, w.Y, d ? w.asq : nullptr))) return rc;
     if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT))) return rc;
     for (int it = 0; it < niter; ++it) {
-      if ((rc = skc(st, 3, A, B, n, m, w.QT, w.Z, w))) return rc;
+      if ((rc = skc(st, A, B, n, m, w.QT, w.Z, w))) return rc;
       if ((rc = orth(st, w.Z, w.Zq, w.V, B, m, r, passes, w, w.XT))) return rc;
-      if ((rc = skr(st, 3, A, B, n, m, w.XT, w.Y, nullptr))) return rc;
+      if ((rc = skr(st, A, B, n, m, w.XT, w.Y, nullptr))) return rc;
       if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT))) return rc;
     }
-    if ((rc = skc(st, 3, A, B, n, m, w.QT, w.Bt, w))) return rc;
+    if ((rc = skc(st, A, B, n, m, w.QT, w.Bt, w))) return rc;
   } else {
     // Y = A Omega (and ||A||^2 partials) ; Q = orth(Y)
     if ((rc = sg(st, SG_ROWSTREAM, A, B, n, m, Omega, r, r, (long long)m * r, w.Y,
