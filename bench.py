@@ -99,9 +99,8 @@ def polar_step(fac, stacks, bd_step, ns_steps, events=None):
     for A, (U, kvec, _) in zip(stacks, res):
         if DB._GATE_ACC[0] is None:
             DB._GATE_ACC[0] = torch.zeros(3, dtype=torch.int64, device=A.device)
-        DB._GATE_ACC[0] += torch.stack([
-            torch.tensor(A.shape[0], dtype=torch.int64, device=A.device),
-            (kvec > 0).sum(), kvec.sum().to(torch.int64)])
+        DB._GATE_ACC[0][0] += A.shape[0]   # host scalar: no host->device copy, no wait
+        DB._GATE_ACC[0][1:] += torch.stack([(kvec > 0).sum(), kvec.sum().to(torch.int64)])
         outs.append((U, kvec))
     return outs
 

@@ -167,15 +167,23 @@ __global__ __launch_bounds__(256) void gram_partials(const float* __restrict__ Y
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int c = 0; c < 4; ++c) g[a][c] = 0.0;
-  for (int base = lo; base < hi; base += 64) {
-    __syncthreads();
+  // the next 64-row block is loaded into registers while the current one is used
+  float nx[16];
+  auto load = [&](int base) {
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int e = tid + 256 * u;
       const int row = base + (e >> 6);
-      Ys[e] = row < hi ? Y[(long long)row * RP + (e & 63)] : 0.f;
+      nx[u] = row < hi ? Y[(long long)row * RP + (e & 63)] : 0.f;
     }
+  };
+  if (lo < hi) load(lo);
+  for (int base = lo; base < hi; base += 64) {
     __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 16; ++u) Ys[tid + 256 * u] = nx[u];
+    __syncthreads();
+    if (base + 64 < hi) load(base + 64);
     const int nr = min(64, hi - base);
     for (int rr = 0; rr < nr; ++rr) {
       const float4 x = *(const float4*)&Ys[rr * RP + 4 * bi];
@@ -217,27 +225,46 @@ __device__ __forceinline__ double lane_val(double v, int lane) {
   return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// One wavefront per matrix, everything in registers: lane l holds row l of the
-// (identity-padded) Gram, the factorization and the inversion are fully unrolled
-// over the 64 x 64 problem, and values of other rows arrive by readlane.
-__global__ __launch_bounds__(64) void chol_inv(const double* __restrict__ part, int r,
-                                               float* __restrict__ M, int* __restrict__ degen) {
-  const int b = blockIdx.x, l = threadIdx.x;
-  __shared__ double Ls[RP][RP + 1];
+// One wavefront per matrix.  Lane l keeps row l of the (identity-padded) Gram in
+// registers; the factorization and the inversion are fully unrolled over the 64 x 64
+// problem.  Step k of the right-looking Cholesky broadcasts the pivot by readlane and
+// the new column L[k.., k] through LDS (lane i writes L[i][k]; every lane then reads
+// the column with broadcast LDS reads, which keep the values in VGPRs).  Entries right
+// of the diagonal of a lane's row are updated too (their values are never read), which
+// keeps the update free of per-lane predication.  Then L goes to LDS by rows and lane
+// l computes column l of L^-1 by forward substitution.
+constexpr int CHOL_THREADS = 256;   // all sum the Gram partials; wave 0 factors
+
+__global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restrict__ part, int r,
+                                                         float* __restrict__ M,
+                                                         int* __restrict__ degen) {
+  constexpr int LP = RP + 2;   // row pitch (doubles): 16-byte aligned rows, 4-way at most
+  constexpr int PER = RP * RP / CHOL_THREADS;
+  const int b = blockIdx.x, tid = threadIdx.x, l = tid & 63;
+  __shared__ __attribute__((aligned(16))) double Ls[RP * LP];   // Gram, then L by rows
+  __shared__ __attribute__((aligned(16))) double Lc[RP * RP];   // row k: column k of L
   {
+    // every load of the partials issued up front (summed in chunk order)
     const double* pb = part + (long long)b * GRAM_CHUNKS * RP * RP;
-    for (int e = l; e < RP * RP; e += 64) {
-      double acc = 0.0;
+    double acc[PER];
 #pragma unroll
-      for (int c = 0; c < GRAM_CHUNKS; ++c) acc += pb[(long long)c * RP * RP + e];
+    for (int u = 0; u < PER; ++u) acc[u] = 0.0;
+#pragma unroll
+    for (int c = 0; c < GRAM_CHUNKS; ++c)
+#pragma unroll
+      for (int u = 0; u < PER; ++u) acc[u] += pb[(long long)c * RP * RP + tid + CHOL_THREADS * u];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int e = tid + CHOL_THREADS * u;
       const int i = e / RP, j = e % RP;
-      Ls[i][j] = (i < r && j < r) ? acc : (i == j ? 1.0 : 0.0);
+      Ls[i * LP + j] = (i < r && j < r) ? acc[u] : (i == j ? 1.0 : 0.0);
     }
   }
-  __builtin_amdgcn_wave_barrier();
+  __syncthreads();
+  if (tid >= 64) return;
   double g[RP];
 #pragma unroll
-  for (int j = 0; j < RP; ++j) g[j] = Ls[l][j];
+  for (int j = 0; j < RP; ++j) g[j] = Ls[l * LP + j];
   // right-looking Cholesky: after step k, g[k] of lane l >= k holds L[l][k]
   bool fail = false;
 #pragma unroll
@@ -247,31 +274,53 @@ __global__ __launch_bounds__(64) void chol_inv(const double* __restrict__ part, 
     const double lkk = sqrt(dk > 0.0 ? dk : 1.0);
     const double lik = (l > k) ? g[k] / lkk : (l == k ? lkk : 0.0);
     g[k] = lik;
+    if (k + 1 < RP) {
+      Lc[k * RP + l] = lik;
+      // a wave's LDS accesses complete in order: the reads below see every lane's write
+      asm volatile("" ::: "memory");
 #pragma unroll
-    for (int j = k + 1; j < RP; ++j) {
-      const double ljk = lane_val(lik, j);       // L[j][k]
-      if (l >= j) g[j] -= lik * ljk;
+      for (int j = k + 1; j < RP; ++j) {
+        g[j] = fma(-lik, Lc[k * RP + j], g[j]);
+        // keep the update in this step (otherwise the compiler defers it to the
+        // step that needs g[j], holding every loaded column value until then) and
+        // the column loads in batches of 8
+        asm volatile("" : "+v"(g[j]));
+        if ((j & 7) == 7) asm volatile("" ::: "memory");
+      }
     }
   }
-  // L to LDS (row l from lane l); then x = column l of L^-1 by forward
-  // substitution, L[i][i] x_i = delta_il - sum_{t<i} L[i][t] x_t (broadcast reads of L)
+  // L by rows into LDS; x = column l of L^-1 by forward substitution,
+  // L[i][i] x_i = delta_il - sum_{t<i} L[i][t] x_t (broadcast reads of row i of L);
+  // x_i = 0 for i < l
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
-  for (int j = 0; j < RP; ++j) Ls[l][j] = g[j];
-  __builtin_amdgcn_wave_barrier();
+  for (int j = 0; j < RP; ++j) Ls[l * LP + j] = g[j];
+  asm volatile("" ::: "memory");
   double x[RP];
 #pragma unroll
   for (int i = 0; i < RP; ++i) {
-    double sacc = (i == l) ? 1.0 : 0.0;
+    double s0 = (i == l) ? 1.0 : 0.0, s1 = 0.0;
 #pragma unroll
-    for (int t = 0; t < i; ++t) sacc -= Ls[i][t] * x[t];
-    x[i] = (i < l) ? 0.0 : sacc / Ls[i][i];
+    for (int t = 0; t + 1 < i; t += 2) {
+      s0 = fma(-Ls[i * LP + t], x[t], s0);
+      s1 = fma(-Ls[i * LP + t + 1], x[t + 1], s1);
+      if ((t & 7) == 6) asm volatile("" ::: "memory");   // row loads in batches of 8
+    }
+    if (i & 1) s0 = fma(-Ls[i * LP + i - 1], x[i - 1], s0);
+    x[i] = (i < l) ? 0.0 : (s0 + s1) / Ls[i * LP + i];
   }
-  // M = L^-T: M[a][c] = (L^-1)[c][a] = x_c of lane a... lane l holds column l of L^-1,
-  // i.e. row l of M
+  // M = L^-T: M[a][c] = (L^-1)[c][a], so row l of M is x
   float* Mb = M + (long long)b * RP * RP + (long long)l * RP;
 #pragma unroll
-  for (int c = 0; c < RP; ++c) Mb[c] = (!fail && l < r && c < r) ? (float)x[c] : 0.f;
+  for (int c = 0; c < RP; c += 4) {
+    float4 v;
+    v.x = (!fail && l < r && c < r) ? (float)x[c] : 0.f;
+    v.y = (!fail && l < r && c + 1 < r) ? (float)x[c + 1] : 0.f;
+    v.z = (!fail && l < r && c + 2 < r) ? (float)x[c + 2] : 0.f;
+    v.w = (!fail && l < r && c + 3 < r) ? (float)x[c + 3] : 0.f;
+    *(float4*)&Mb[c] = v;
+  }
   if (l == 0 && degen && fail) degen[b] = 1;
 }
 
@@ -418,23 +467,64 @@ constexpr int SK_PITCH = SK_KC + 8;
 constexpr int SK_TERM = RP * SK_PITCH;       // bf16 per split term
 constexpr int SK_BUF = 3 * SK_TERM;          // bf16 per chunk buffer (up to 3 terms)
 
+// Loads of the skinny products go through buffer descriptors: a load whose byte offset
+// is at or beyond the descriptor's size returns zeros without touching memory.  Offsets
+// outside a matrix (rows beyond n, indices beyond m, steps past the end) are set to
+// SK_OOB, so every load is unconditional: no branches, and the compiler can count the
+// loads in flight across steps.  The host keeps every operand below 2^31 bytes.
+constexpr unsigned SK_OOB = 0xF0000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const float* p, long long elems) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)(elems * 4), 0x00020000);
+}
+__device__ __forceinline__ float4 sk_ld4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ float2 sk_ld2(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+// A copy the compiler cannot fold away: a prefetch slot is copied out before its next
+// load is issued into the same registers, so the loop carries the slot in place and no
+// register move of in-flight data (which would wait for the load) is needed at the
+// loop's back edge.
+__device__ __forceinline__ float sk_mov(float x) {
+  float y;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(x));
+  return y;
+}
+__device__ __forceinline__ float4 sk_mov(float4 x) {
+  return make_float4(sk_mov(x.x), sk_mov(x.y), sk_mov(x.z), sk_mov(x.w));
+}
+__device__ __forceinline__ float2 sk_mov(float2 x) { return make_float2(sk_mov(x.x), sk_mov(x.y)); }
+
 // Thread t stages the units u = t and t + 256 of a chunk: row c = u / 8, contraction
 // indices k0 + 8 (u % 8) .. +7 (zero at and beyond kend; 8-index groups are whole).
 struct SkStage {
   float4 v[2][2];
 };
 
-__device__ __forceinline__ void sk_stage_load(SkStage& st, const float* __restrict__ S, int lds,
+__device__ __forceinline__ void sk_stage_load(SkStage& st, __amdgpu_buffer_rsrc_t sr, int lds,
                                               int k0, int kend, int tid) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int u = tid + 256 * q;
     const int c = u >> 3, k = k0 + 8 * (u & 7);
-    const bool ok = k < kend;
-    const float* p = S + (long long)c * lds + (ok ? k : 0);
-    st.v[q][0] = ok ? *(const float4*)p : make_float4(0.f, 0.f, 0.f, 0.f);
-    st.v[q][1] = ok ? *(const float4*)(p + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const unsigned off = k < kend ? (unsigned)(c * lds + k) * 4u : SK_OOB;
+    st.v[q][0] = sk_ld4(sr, off);
+    st.v[q][1] = sk_ld4(sr, off + 16u);
   }
+}
+
+// Keeps the split of a staged chunk at the point of this call: without it the compiler
+// hoists the split to the top of the loop, where it waits for the staging loads just
+// issued and with them for every prefetched load of A.
+__device__ __forceinline__ void sk_pin(SkStage& st) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      asm volatile("" : "+v"(st.v[q][h].x), "+v"(st.v[q][h].y), "+v"(st.v[q][h].z),
+                   "+v"(st.v[q][h].w));
 }
 
 template <int SPLITS>
@@ -491,13 +581,15 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
   A += (long long)b * n * m;
   XT += (long long)b * RP * ldxt;
   C += (long long)b * n * RP;
-  const float* ap[2];
+  const __amdgpu_buffer_rsrc_t ar = sk_rsrc(A, (long long)n * m);
+  const __amdgpu_buffer_rsrc_t xr = sk_rsrc(XT, (long long)RP * ldxt);
   bool ain[2];
+  unsigned abase[2];   // byte offset of the lane's first float, SK_OOB for rows >= n
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const int i = r0 + 32 * rb + l32;
     ain[rb] = i < n;
-    ap[rb] = A + (long long)(ain[rb] ? i : 0) * m + 16 * hk;
+    abase[rb] = ain[rb] ? (unsigned)(i * m + 16 * hk) * 4u : SK_OOB;
   }
   f32x16 acc[2][2];
 #pragma unroll
@@ -507,9 +599,9 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[rb][cb][e] = 0.f;
   double sq = 0.0;
-  const int nk = (m + 31) / 32;             // 32-index steps
   const int nch = (m + SK_KC - 1) / SK_KC;  // staged chunks
   // floats 8 q .. 8 q + 7 of the lane's 16 at step ks: indices 32 ks + 16 hk + 8 q ..
+  // (a step at or past nk loads zeros)
   auto load = [&](int ks, float4 (&a)[2][4]) {
     const int k = 32 * ks;
 #pragma unroll
@@ -517,29 +609,31 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
       const bool kin = k + 16 * hk + 4 * v < m;   // m % 8 == 0: 8-index groups are whole
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
-        a[rb][v] = (kin && ain[rb]) ? *(const float4*)(ap[rb] + k + 4 * v)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+        a[rb][v] = sk_ld4(ar, kin ? abase[rb] + (unsigned)(k + 4 * v) * 4u : SK_OOB);
     }
   };
   SkStage stg;
-  sk_stage_load(stg, XT, ldxt, 0, m, tid);
+  sk_stage_load(stg, xr, ldxt, 0, m, tid);
   sk_stage_store<SPLITS>(stg, xl, tid);
-  if (nch > 1) sk_stage_load(stg, XT, ldxt, SK_KC, m, tid);
-  float4 an[2][4];
-  load(0, an);
+  sk_stage_load(stg, xr, ldxt, SK_KC, m, tid);
+  // A two steps ahead: slot p holds step 2 ch + p (SK_KC / 32 == 2 steps per chunk)
+  static_assert(SK_KC == 64, "two A slots per staged chunk");
+  float4 ab[2][2][4];
+  load(0, ab[0]);
+  load(1, ab[1]);
   sk_barrier();
   for (int ch = 0; ch < nch; ++ch) {
     const bf16* buf = xl + (ch & 1) * SK_BUF;
 #pragma unroll
-    for (int p = 0; p < SK_KC / 32; ++p) {
-      const int ks = ch * (SK_KC / 32) + p;
-      if (ks >= nk) break;
+    for (int p = 0; p < 2; ++p) {
+      // a step past nk (the end of a partial last chunk) multiplies zeros
+      const int ks = 2 * ch + p;
       float4 ac[2][4];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) ac[rb][v] = an[rb][v];
-      if (ks + 1 < nk) load(ks + 1, an);
+        for (int v = 0; v < 4; ++v) ac[rb][v] = sk_mov(ab[p][rb][v]);
+      load(ks + 2, ab[p]);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         bf16x8 as[2][SPLITS], xs[2][SPLITS];
@@ -563,11 +657,12 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
             acc[rb][cb] = mfma_split<SPLITS>(xs[cb], as[rb], acc[rb][cb]);
       }
     }
-    if (ch + 1 < nch) {
-      sk_stage_store<SPLITS>(stg, xl + ((ch + 1) & 1) * SK_BUF, tid);
-      sk_barrier();
-      if (ch + 2 < nch) sk_stage_load(stg, XT, ldxt, (ch + 2) * SK_KC, m, tid);
-    }
+    // (after the last chunk this stages zeros nobody reads: no branch in the loop, so
+    // the compiler keeps the prefetched loads in flight across iterations)
+    sk_pin(stg);
+    sk_stage_store<SPLITS>(stg, xl + ((ch + 1) & 1) * SK_BUF, tid);
+    sk_barrier();
+    sk_stage_load(stg, xr, ldxt, (ch + 2) * SK_KC, m, tid);
   }
   // D[c][i] = C[i][c]: lane holds rows c = 32 cb + 8 g + 4 hk + q of column i = l32
 #pragma unroll
@@ -622,33 +717,39 @@ __global__ __launch_bounds__(256) void sk_cols(const float* __restrict__ A, int 
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[e][cb][v] = 0.f;
-  const int nk = (ie - ib + 15) / 16;
   const int nch = (ie - ib + SK_KC - 1) / SK_KC;
+  const __amdgpu_buffer_rsrc_t ar = sk_rsrc(A, (long long)n * m);
+  const __amdgpu_buffer_rsrc_t yr = sk_rsrc(YT, (long long)RP * ldyt);
+  // rows ib + 16 ks + 8 hk .. +7 of the lane's two columns (a step at or past nk, or a
+  // column beyond m, loads zeros)
+  const unsigned cbase = jin ? (unsigned)jl * 4u : SK_OOB;
   auto load = [&](int ks, float2 (&a)[8]) {
     const int i0 = ib + 16 * ks + 8 * hk;
     const bool iin = i0 < ie;            // 8-row groups are whole
 #pragma unroll
     for (int t = 0; t < 8; ++t)
-      a[t] = (iin && jin) ? *(const float2*)(A + (long long)(i0 + t) * m + jl)
-                          : make_float2(0.f, 0.f);
+      a[t] = sk_ld2(ar, iin ? cbase + (unsigned)((i0 + t) * m) * 4u : SK_OOB);
   };
   SkStage stg;
-  sk_stage_load(stg, YT, ldyt, ib, ie, tid);
+  sk_stage_load(stg, yr, ldyt, ib, ie, tid);
   sk_stage_store<SPLITS>(stg, yl, tid);
-  if (nch > 1) sk_stage_load(stg, YT, ldyt, ib + SK_KC, ie, tid);
-  float2 an[8];
-  load(0, an);
+  sk_stage_load(stg, yr, ldyt, ib + SK_KC, ie, tid);
+  // A two substeps ahead: slot p & 1 holds substep ks (SK_KC / 16 == 4 per chunk)
+  static_assert(SK_KC % 32 == 0, "an even number of A substeps per staged chunk");
+  float2 ab[2][8];
+  load(0, ab[0]);
+  load(1, ab[1]);
   sk_barrier();
   for (int ch = 0; ch < nch; ++ch) {
     const bf16* buf = yl + (ch & 1) * SK_BUF;
 #pragma unroll
     for (int p = 0; p < SK_KC / 16; ++p) {
+      // a substep past nk (the end of a partial last chunk) multiplies zeros
       const int ks = ch * (SK_KC / 16) + p;
-      if (ks >= nk) break;
       float2 ac[8];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) ac[t] = an[t];
-      if (ks + 1 < nk) load(ks + 1, an);
+      for (int t = 0; t < 8; ++t) ac[t] = sk_mov(ab[p & 1][t]);
+      load(ks + 2, ab[p & 1]);
       bf16x8 as[2][SPLITS], ys[2][SPLITS];
       {
         const float v0[8] = {ac[0].x, ac[1].x, ac[2].x, ac[3].x, ac[4].x, ac[5].x, ac[6].x, ac[7].x};
@@ -662,11 +763,11 @@ __global__ __launch_bounds__(256) void sk_cols(const float* __restrict__ A, int 
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) acc[e][cb] = mfma_split<SPLITS>(ys[cb], as[e], acc[e][cb]);
     }
-    if (ch + 1 < nch) {
-      sk_stage_store<SPLITS>(stg, yl + ((ch + 1) & 1) * SK_BUF, tid);
-      sk_barrier();
-      if (ch + 2 < nch) sk_stage_load(stg, YT, ldyt, ib + (ch + 2) * SK_KC, ie, tid);
-    }
+    // (after the last chunk this stages zeros nobody reads: no branch in the loop)
+    sk_pin(stg);
+    sk_stage_store<SPLITS>(stg, yl + ((ch + 1) & 1) * SK_BUF, tid);
+    sk_barrier();
+    sk_stage_load(stg, yr, ldyt, ib + (ch + 2) * SK_KC, ie, tid);
   }
   // D[c][col] = C[j][c], col = l32 -> j = j0 + 2 l32 + e
   float* pb = part + ((long long)s * nb + b) * m * RP;
@@ -782,6 +883,7 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
   const int r = gp.r;
   {
     const double* pb = part + (long long)b * GRAM_CHUNKS * RP * RP;
+#pragma unroll
     for (int e = tid; e < RP * RP; e += EG_THREADS) {
       const int i = e / RP, j = e % RP;
       double acc = 0.0;
@@ -1203,7 +1305,12 @@ static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // The split-bf16 skinny GEMMs need m and n to be multiples of 8; other shapes run the
 // fp32-MFMA kernels.
-static bool sk_fast(int n, int m) { return n % 8 == 0 && m % 8 == 0; }
+// The split-bf16 skinny products: shapes they cover (their buffer-descriptor offsets
+// are 32-bit, below SK_OOB).
+static bool sk_fast(int n, int m) {
+  return n % 8 == 0 && m % 8 == 0 && (long long)n * m * 4 < (1LL << 31) &&
+         (long long)RP * n * 4 < (1LL << 31);
+}
 
 static int zero_ints(hipStream_t st, int* p, int count) {
   if (count <= 0) return DMH_OK;
@@ -1313,7 +1420,7 @@ static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int
     const bool last = p == passes - 1;
     float* dst = last ? Q : (p % 2 == 0 ? tmp : Q);
     if ((rc = gram(st, src, B, rows, w.gram))) return rc;
-    hipLaunchKernelGGL(chol_inv, dim3(B), dim3(64), 0, st, w.gram, r, w.M, w.degen);
+    hipLaunchKernelGGL(chol_inv, dim3(B), dim3(CHOL_THREADS), 0, st, w.gram, r, w.M, w.degen);
     DMH_CHECK_LAUNCH("chol_inv");
     hipLaunchKernelGGL(right_mult, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, src, rows,
                        (long long)rows * RP, w.M, dst, (long long)rows * RP,

@@ -244,9 +244,11 @@ class Muon(torch.optim.Optimizer):
         for (shape, es), A, (Ug, kvec, _) in zip(groups, As, results):
             if _GATE_ACC[0] is None or _GATE_ACC[0].device != kvec.device:
                 _GATE_ACC[0] = torch.zeros(3, dtype=torch.int64, device=kvec.device)
-            _GATE_ACC[0] += torch.stack([
-                torch.tensor(A.shape[0], dtype=torch.int64, device=kvec.device),
-                (kvec > 0).sum(), kvec.sum().to(torch.int64)])
+            # the same tick as muon.py:306-308, with the matrix count added as a host
+            # scalar: a torch.tensor(..., device=gpu) copy would block the host until
+            # the stream drains (the whole polar step), every optimizer step
+            _GATE_ACC[0][0] += A.shape[0]
+            _GATE_ACC[0][1:] += torch.stack([(kvec > 0).sum(), kvec.sum().to(torch.int64)])
             if fused:
                 _native.apply_update(self._glue_params(es, shape, lr, weight_decay, group), Ug)
                 continue
