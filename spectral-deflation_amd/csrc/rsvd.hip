@@ -831,10 +831,15 @@ struct GateParams {
   float ratio, thresh, pad;
 };
 
-constexpr int JP = RP + 1;   // LDS pitch
+constexpr int JP = RP + 2;   // H row pitch (doubles): rows 16-byte aligned
 constexpr int NPAIR = RP / 2;
-constexpr int EG_THREADS = 256;
-constexpr int EG_BLOCKS = NPAIR * (NPAIR + 1) / 2;   // 2x2 blocks (t <= u)
+constexpr int EG_THREADS = 512;
+constexpr int EG_WAVES = EG_THREADS / 64;
+constexpr int EG_OFF = NPAIR * (NPAIR - 1) / 2;   // off-diagonal 2x2 blocks (t < u)
+constexpr int VR = RP / EG_WAVES;                 // rows of V per wave
+static_assert(EG_OFF <= EG_THREADS && EG_OFF > EG_THREADS - 64,
+              "one off-diagonal block per thread, the last wave partly idle");
+static_assert(VR * EG_WAVES == RP, "V rows split evenly over the waves");
 
 // next-round position of the element at position x (inverse of the seat move)
 __device__ __forceinline__ int jac_next(int x) {
@@ -872,10 +877,11 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
                                                        const double* __restrict__ qpart,
                                                        const double* __restrict__ asq, int asq_n,
                                                        float* __restrict__ d_out) {
-  __shared__ double Hs[2][RP * JP];
-  __shared__ float Vs[2][RP * JP];        // eigenvectors (accumulated rotations), fp32
-  __shared__ double ang[4][3][NPAIR];     // per-wave copy of the round's cos, sin, tan
-  __shared__ int perm[2][RP];             // original index of each position
+  __shared__ __attribute__((aligned(16))) double Hs[2][RP * JP];   // upper triangle in use
+  // per wave: c, s, tan of pair t in slot t (slots 32.. take the duplicates of lanes 32..)
+  __shared__ __attribute__((aligned(16))) double ang[EG_WAVES][64][4];
+  __shared__ float Vf[RP * (RP + 1)];     // eigenvectors at the end, column = original index
+  __shared__ int perm[3][RP];             // original index of each position (3 rounds)
   __shared__ double s_tr;
   __shared__ int order[RP];
   __shared__ float sv[RP];
@@ -890,7 +896,6 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
 #pragma unroll
       for (int c = 0; c < GRAM_CHUNKS; ++c) acc += pb[(long long)c * RP * RP + e];
       Hs[0][i * JP + j] = (i < r && j < r) ? acc : 0.0;
-      Vs[0][i * JP + j] = (i == j) ? 1.f : 0.f;
     }
     if (tid < RP) perm[0][tid] = tid;
   }
@@ -907,120 +912,111 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
   __syncthreads();
   const double floor_pq = 1e-15 * s_tr;
 
-  // this thread's 2x2 blocks: blk -> (t, u), t <= u; read offsets (current
-  // buffer) and write offsets (next buffer, through the seat move)
-  int nb = 0;
-  int ro[3][4], wo[3][4], bt[3], bu[3];
+  // H: only the upper triangle (row <= column) is read and written after the load.
+  // Thread T < EG_OFF rotates the off-diagonal block (t, u), t < u, with u running
+  // fastest over consecutive threads (contiguous LDS rows); lanes 0..31 of the last
+  // wave also write the diagonal blocks, from their angle computation.  Read offsets
+  // (current buffer) and write offsets (next buffer, through the seat move, folded
+  // into the upper triangle) are fixed per thread.
+  auto up = [](int i, int j) { return i <= j ? i * JP + j : j * JP + i; };
+  int bt = 0, bu = 0, rp = 0, rq = 0, wr[4] = {0, 0, 0, 0}, dw[3];
+  if (tid < EG_OFF) {
+    int t = 0, rem = tid;
+    while (rem >= NPAIR - 1 - t) { rem -= NPAIR - 1 - t; ++t; }
+    bt = t;
+    bu = t + 1 + rem;
+    const int p = 2 * bt, q = p + 1, p2 = 2 * bu, q2 = p2 + 1;
+    rp = p * JP + p2;   // (p, p2), (p, q2)
+    rq = q * JP + p2;   // (q, p2), (q, q2)
+    const int np_ = jac_next(p), nq = jac_next(q), np2 = jac_next(p2), nq2 = jac_next(q2);
+    wr[0] = up(np_, np2); wr[1] = up(np_, nq2); wr[2] = up(nq, np2); wr[3] = up(nq, nq2);
+  }
+  {
+    const int t = l & (NPAIR - 1), p = 2 * t, q = p + 1;
+    dw[0] = up(jac_next(p), jac_next(p));
+    dw[1] = up(jac_next(p), jac_next(q));
+    dw[2] = up(jac_next(q), jac_next(q));
+  }
+  const bool diag_writer = wave == EG_WAVES - 1 && l < NPAIR;
+  // V (the accumulated rotations) in registers: lane l holds column l (the original
+  // index l, which never moves) for rows VR wave .. VR wave + VR - 1.  A round rotates
+  // the columns of the position pairs (2t, 2t + 1): lane l finds its position and its
+  // partner's original index in perm and takes the partner's values by a lane shuffle,
+  // so V costs no LDS traffic.  V's update for a round runs at the start of the next
+  // one, beside that round's angle computation (the two are independent, and both
+  // are latency chains); perm is kept for three rounds for it.
+  float v[VR];
 #pragma unroll
-  for (int x = 0; x < 3; ++x) {
-    const int blk = tid + EG_THREADS * x;
-    bt[x] = bu[x] = 0;
+  for (int i = 0; i < VR; ++i) v[i] = (VR * wave + i == l) ? 1.f : 0.f;
+  int pos = l, pb = 0;
+  // the previous round: position, angles (lanes 0..31), perm buffer; the first
+  // update is the identity (c = 1, s = 0)
+  int ppos = l, ppb = 0;
+  float pcf = 1.f, psf = 0.f;
+  auto vstep = [&]() {
+    const int pc = perm[ppb][ppos ^ 1];   // the partner's original index (= its lane)
+    const float c = __shfl(pcf, ppos >> 1), s = __shfl(psf, ppos >> 1);
+    const bool isp = (ppos & 1) == 0;
 #pragma unroll
-    for (int y = 0; y < 4; ++y) ro[x][y] = wo[x][y] = 0;
-    if (blk < EG_BLOCKS) {
-      int u = (int)((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
-      while ((u + 1) * (u + 2) / 2 <= blk) ++u;
-      while (u * (u + 1) / 2 > blk) --u;
-      const int t = blk - u * (u + 1) / 2;
-      bt[x] = t; bu[x] = u;
-      const int p = 2 * t, q = 2 * t + 1, p2 = 2 * u, q2 = 2 * u + 1;
-      ro[x][0] = p * JP + p2; ro[x][1] = p * JP + q2; ro[x][2] = q * JP + p2; ro[x][3] = q * JP + q2;
-      const int np_ = jac_next(p), nq = jac_next(q), np2 = jac_next(p2), nq2 = jac_next(q2);
-      wo[x][0] = np_ * JP + np2; wo[x][1] = np_ * JP + nq2; wo[x][2] = nq * JP + np2; wo[x][3] = nq * JP + nq2;
-      nb = x + 1;
+    for (int i = 0; i < VR; ++i) {
+      const float o = __shfl(v[i], pc);
+      v[i] = isp ? c * v[i] - s * o : s * o + c * v[i];
     }
-  }
-  // V items: row vrow, pairs vt0 + 4k, k < 8
-  const int vrow = tid & 63, vt0 = tid >> 6;
-  const int vrd = vrow * JP;
-  int vwp[NPAIR / 4], vwq[NPAIR / 4];
-#pragma unroll
-  for (int k = 0; k < NPAIR / 4; ++k) {
-    const int t = vt0 + 4 * k;
-    vwp[k] = vrd + jac_next(2 * t);
-    vwq[k] = vrd + jac_next(2 * t + 1);
-  }
+  };
 
   int cur = 0;
   for (int sweep = 0; sweep < 40; ++sweep) {
     for (int rd = 0; rd < RP - 1; ++rd) {
       const double* Hc = Hs[cur];
-      // angles of the round (every wave, lanes 0..31: pair t = lane)
-      if (l < NPAIR) {
-        const double hpp = Hc[(2 * l) * JP + 2 * l], hpq = Hc[(2 * l) * JP + 2 * l + 1];
-        const double hqq = Hc[(2 * l + 1) * JP + 2 * l + 1];
-        double c = 1.0, sn = 0.0, tn = 0.0;
-        if (hpq * hpq > 1e-24 * fabs(hpp * hqq) && fabs(hpq) > floor_pq) {
-          const double theta = (hqq - hpp) * (0.5 * rcp_nr(hpq));
-          const double th2 = theta * theta;
-          // |theta| + sqrt(1 + theta^2)
-          const double den = fabs(theta) + (1.0 + th2) * rsqrt_nr(1.0 + th2);
-          tn = (theta >= 0 ? 1.0 : -1.0) * rcp_nr(den);
-          c = rsqrt_nr(1.0 + tn * tn);
-          sn = tn * c;
+      double* Hn = Hs[cur ^ 1];
+      vstep();
+      // angles of the round, every lane without branches (lane l: pair l % 32)
+      float cf, sf;
+      {
+        const int t = l & (NPAIR - 1);
+        const double2 pq = *(const double2*)&Hc[(2 * t) * JP + 2 * t];   // h_pp, h_pq
+        const double hpp = pq.x, hpq = pq.y;
+        const double hqq = Hc[(2 * t + 1) * JP + 2 * t + 1];
+        const bool rot = hpq * hpq > 1e-24 * fabs(hpp * hqq) && fabs(hpq) > floor_pq;
+        const double theta = (hqq - hpp) * (0.5 * rcp_nr(rot ? hpq : 1.0));
+        const double th2 = theta * theta;
+        // |theta| + sqrt(1 + theta^2)
+        const double den = fabs(theta) + (1.0 + th2) * rsqrt_nr(1.0 + th2);
+        const double tr_ = (theta >= 0 ? 1.0 : -1.0) * rcp_nr(den);
+        const double cr_ = rsqrt_nr(1.0 + tr_ * tr_);
+        const double c = rot ? cr_ : 1.0, sn = rot ? tr_ * cr_ : 0.0, tn = rot ? tr_ : 0.0;
+        *(double2*)&ang[wave][l][0] = make_double2(c, sn);
+        ang[wave][l][2] = tn;
+        cf = (float)c;
+        sf = (float)sn;
+        if (diag_writer) {   // the diagonal block of pair t (Golub-Van Loan update)
+          Hn[dw[0]] = hpp - tn * hpq;
+          Hn[dw[1]] = tn == 0.0 ? hpq : 0.0;   // unrotated pairs keep h_pq
+          Hn[dw[2]] = hqq + tn * hpq;
         }
-        ang[wave][0][l] = c;
-        ang[wave][1][l] = sn;
-        ang[wave][2][l] = tn;
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's angles are in LDS
-      double* Hn = Hs[cur ^ 1];
-      const float* Vc = Vs[cur];
-      float* Vn = Vs[cur ^ 1];
-      // loads first (H blocks, V pairs, angles), then the arithmetic and stores
-      double xv[3][4], a_c[3][2], a_s[3][2], a_t[3];
-#pragma unroll
-      for (int x = 0; x < 3; ++x) {
-        if (x < nb) {
-#pragma unroll
-          for (int y = 0; y < 4; ++y) xv[x][y] = Hc[ro[x][y]];
-          a_c[x][0] = ang[wave][0][bt[x]]; a_s[x][0] = ang[wave][1][bt[x]];
-          a_c[x][1] = ang[wave][0][bu[x]]; a_s[x][1] = ang[wave][1][bu[x]];
-          a_t[x] = ang[wave][2][bt[x]];
-        }
+      if (tid < EG_OFF) {
+        const double2 xp = *(const double2*)&Hc[rp], xq = *(const double2*)&Hc[rq];
+        const double2 a1 = *(const double2*)&ang[wave][bt][0];
+        const double2 a2 = *(const double2*)&ang[wave][bu][0];
+        const double c1 = a1.x, s1 = a1.y, c2 = a2.x, s2 = a2.y;
+        // rows: R_t^T X, then columns: (R_t^T X) R_u
+        const double y00 = c1 * xp.x - s1 * xq.x, y01 = c1 * xp.y - s1 * xq.y;
+        const double y10 = s1 * xp.x + c1 * xq.x, y11 = s1 * xp.y + c1 * xq.y;
+        Hn[wr[0]] = c2 * y00 - s2 * y01;
+        Hn[wr[1]] = s2 * y00 + c2 * y01;
+        Hn[wr[2]] = c2 * y10 - s2 * y11;
+        Hn[wr[3]] = s2 * y10 + c2 * y11;
       }
-      float vp[NPAIR / 4], vq[NPAIR / 4], vc[NPAIR / 4], vs[NPAIR / 4];
-#pragma unroll
-      for (int k = 0; k < NPAIR / 4; ++k) {
-        const int t = vt0 + 4 * k;
-        vp[k] = Vc[vrd + 2 * t];
-        vq[k] = Vc[vrd + 2 * t + 1];
-        vc[k] = (float)ang[wave][0][t];
-        vs[k] = (float)ang[wave][1][t];
+      const int nb = pb == 2 ? 0 : pb + 1;
+      if (l < RP / EG_WAVES) {
+        const int x = (RP / EG_WAVES) * wave + l;
+        perm[nb][jac_next(x)] = perm[pb][x];
       }
-#pragma unroll
-      for (int x = 0; x < 3; ++x) {
-        if (x < nb) {
-          double z00, z01, z10, z11;
-          if (bt[x] == bu[x]) {
-            // xv = [[h_pp, h_pq], [h_qp, h_qq]]
-            z00 = xv[x][0] - a_t[x] * xv[x][1];
-            z11 = xv[x][3] + a_t[x] * xv[x][1];
-            z01 = z10 = a_t[x] == 0.0 ? xv[x][1] : 0.0;   // unrotated pairs keep h_pq
-          } else {
-            const double c1 = a_c[x][0], s1 = a_s[x][0], c2 = a_c[x][1], s2 = a_s[x][1];
-            // rows: R_t^T X, then columns: (R_t^T X) R_u
-            const double y00 = c1 * xv[x][0] - s1 * xv[x][2], y01 = c1 * xv[x][1] - s1 * xv[x][3];
-            const double y10 = s1 * xv[x][0] + c1 * xv[x][2], y11 = s1 * xv[x][1] + c1 * xv[x][3];
-            z00 = c2 * y00 - s2 * y01; z01 = s2 * y00 + c2 * y01;
-            z10 = c2 * y10 - s2 * y11; z11 = s2 * y10 + c2 * y11;
-          }
-          Hn[wo[x][0]] = z00; Hn[wo[x][1]] = z01; Hn[wo[x][2]] = z10; Hn[wo[x][3]] = z11;
-          if (bt[x] != bu[x]) {   // mirror: (row, col) -> (col, row) in the next buffer
-            const int w00 = wo[x][0], w01 = wo[x][1], w10 = wo[x][2], w11 = wo[x][3];
-            Hn[(w00 % JP) * JP + w00 / JP] = z00;
-            Hn[(w01 % JP) * JP + w01 / JP] = z01;
-            Hn[(w10 % JP) * JP + w10 / JP] = z10;
-            Hn[(w11 % JP) * JP + w11 / JP] = z11;
-          }
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < NPAIR / 4; ++k) {
-        Vn[vwp[k]] = vc[k] * vp[k] - vs[k] * vq[k];
-        Vn[vwq[k]] = vs[k] * vp[k] + vc[k] * vq[k];
-      }
-      if (tid < RP) perm[cur ^ 1][jac_next(tid)] = perm[cur][tid];
+      ppos = pos; ppb = pb; pcf = cf; psf = sf;
+      pos = jac_next(pos);
+      pb = nb;
       __syncthreads();
       cur ^= 1;
     }
@@ -1036,9 +1032,11 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
     }
     if (!__syncthreads_or(live)) break;
   }
+  vstep();   // the last round's V update
+#pragma unroll
+  for (int i = 0; i < VR; ++i) Vf[(VR * wave + i) * (RP + 1) + l] = v[i];
   const double* H = Hs[cur];
-  const float* V = Vs[cur];
-  const int* pm = perm[cur];
+  const int* pm = perm[pb];
   __syncthreads();
   // sort eigenvalues descending over the real positions (original index < r;
   // stable rank; NaN ranks last)
@@ -1086,7 +1084,7 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
   for (int e = tid; e < RP * RP; e += EG_THREADS) {
     const int a = e / RP, t = e % RP;   // row a of Ub, column t (sorted)
     float u = 0.f;
-    if (a < r && t < r && !bad) u = V[a * JP + order[t]];
+    if (a < r && t < r && !bad) u = Vf[a * (RP + 1) + pm[order[t]]];
     Ubb[e] = u;
     UbSb[e] = sv[t] > 0.f ? u / sv[t] : 0.f;
   }
@@ -1119,11 +1117,11 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
     __builtin_amdgcn_wave_barrier();
     double head = 0.0;
     for (int t = 0; t < kk; ++t) {
-      const int ct = order[t];
+      const int ct = pm[order[t]];   // column of V (original index) of rank t
       double y = 0.0;                       // (Q^T Q Ub_t)_l
       if (l < r)
-        for (int c = 0; c < r; ++c) y = fma(G[l * JP + c], (double)V[c * JP + ct], y);
-      double gt = (l < r) ? (double)V[l * JP + ct] * y : 0.0;
+        for (int c = 0; c < r; ++c) y = fma(G[l * JP + c], (double)Vf[c * (RP + 1) + ct], y);
+      double gt = (l < r) ? (double)Vf[l * (RP + 1) + ct] * y : 0.0;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) gt += __shfl_xor(gt, o);
       const double lam = __shfl(lam_l, t);
