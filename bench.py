@@ -402,21 +402,39 @@ def main():
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
     for s in range(args.steps):
-        step(args.warmup + s + 1, events)
+        step(args.warmup + s + 1, None if not plain else events)
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = start.elapsed_time(stop)
     ms_per_step = gpu_ms / args.steps
+    st = DB.polar_stats()   # gate statistics of the timed steps
+    if not plain:
+        # The timed steps run every group's chain on its own stream, overlapping the
+        # other group's work, so the chains' own time is measured in a second pass of
+        # the same steps with the chains one after the other on the launch stream
+        # (HIP events around each chain call) once both front-ends have finished.
+        log(f"bench: NS-chain pass, {args.steps} steps")
+        events = []
+        seq0 = torch.cuda.Event(enable_timing=True)
+        seq1 = torch.cuda.Event(enable_timing=True)
+        seq0.record()
+        for s in range(args.steps):
+            step(args.warmup + s + 1, events)
+        seq1.record()
+        torch.cuda.synchronize()
+        seq_ms = seq0.elapsed_time(seq1) / args.steps
     ns_ms = sum(e0.elapsed_time(e1) for evs in events for e0, e1 in evs) / args.steps
-    front_ms = ms_per_step - ns_ms   # the groups' front-ends (concurrent) and the gate ticks
+    # plain arms: the chain is the whole step; deflated arms: the front-ends (with the
+    # chains of the sequential pass subtracted) and the gate ticks
+    front_ms = ms_per_step - ns_ms if plain else seq_ms - ns_ms
     if plain:   # the chain is the whole step: same matrices, plain-arm layout
         groups = [(B, max(r_, c_), min(r_, c_)) for B, r_, c_, _ in PLAIN_GROUPS[args.workload]]
-    st = DB.polar_stats()
     flops = ns_flops(groups)
     achieved = flops / (ns_ms * 1e-3) / 1e12
     log(f"bench: {ms_per_step:.3f} ms/step (wall {1e3 * wall / args.steps:.3f}), NS chain "
-        f"{ns_ms:.3f} ms, gate {st}")
+        f"{ns_ms:.3f} ms" + ("" if plain else f" (sequential pass {seq_ms:.3f} ms/step)")
+        + f", gate {st}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -457,7 +475,11 @@ def main():
                      if traffic else None,
                      "kernel": "NS chain (gemm_nt_bf16 K1/K2/K3 launches of a polar step), "
                                "canonical dense 4m^2n+2m^3 FLOP per matrix-iteration",
-                     "flops_per_step": flops, "ns_ms_per_step": ns_ms},
+                     "flops_per_step": flops, "ns_ms_per_step": ns_ms,
+                     "ns_timing": "HIP events around each chain call on the launch stream"
+                                  + ("" if plain else ", in a pass of the same steps with "
+                                     "the chains one after the other (the timed steps "
+                                     "overlap them with the other group's work)")},
         "frontend_ms_per_step": None if plain else front_ms,
         "gate": None if plain else st,
         "cpu_baseline": cpu,

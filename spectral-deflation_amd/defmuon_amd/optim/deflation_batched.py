@@ -196,13 +196,15 @@ class _DeflatedPolarBase:
         """polar_group over the tall shape groups of one optimizer step, with one
         generator per group; returns [(polar factors, k, d)] in group order.
 
-        For the built-in arms the groups' front-ends run concurrently, each on a
-        stream of its own (they are independent, and each alone is a chain of small
-        latency-bound launches that leaves most of the GPU idle), and the chains then
-        run one after the other on the current stream.  Every group's sketch comes
-        from its own generator and every result equals that of a polar_group call.
-        chain_events: optional list of (start, end) torch.cuda.Event pairs, recorded
-        on the current stream around each group's chain."""
+        For the built-in arms every group runs on a stream of its own, its chain right
+        after its front-end: the front-ends are chains of small latency-bound launches
+        that alone leave most of the GPU idle, and the GEMM launches of one group's
+        chain leave partial last rounds of tiles that the other group's work fills.
+        With chain_events (a list of (start, end) torch.cuda.Event pairs, one per group)
+        the chains instead run one after the other on the current stream once every
+        front-end has finished, with pair g recorded around group g's chain, so that
+        the chains' time can be measured alone.  Every group's sketch comes from its
+        own generator and every result equals that of a polar_group call."""
         hs = self._fused(steps)
         if hs is None or len(As) < 2 or not As[0].is_cuda:
             # one group after the other (an arm with its own clip or iteration: the
@@ -220,9 +222,11 @@ class _DeflatedPolarBase:
         dev = As[0].device
         main = torch.cuda.current_stream(dev)
         side = _side_streams(dev, len(As))
-        # the largest front-end (the critical path) is enqueued first
+        concurrent_chains = not chain_events
+        # the largest group (the critical path) is enqueued first
         order = sorted(range(len(As)), key=lambda gi: -As[gi].numel())
         fronts = [None] * len(As)
+        outs = [None] * len(As)
         for s, gi in zip(side, order):
             A, gen = As[gi], generators[gi]
             s.wait_stream(main)
@@ -232,21 +236,24 @@ class _DeflatedPolarBase:
                 Omega = torch.randn(Bn, m, r, device=dev, dtype=A.dtype, generator=gen)
                 fr = _native.deflated_polar_front(A, Omega, kw, GATE_RATIO, DEFLATE_THRESH,
                                                   self.PAD, RSVD_NITER, CHOLQR_PASSES)
+                if concurrent_chains:
+                    U = _native.deflated_polar_chain(fr, hs)
+                    U.record_stream(main)
+                    outs[gi] = (U, fr.k, fr.d)
             A.record_stream(s)
             for t in (fr.ws, fr.k, fr.d):
                 t.record_stream(main)
             fronts[gi] = fr
         for s in side:
             main.wait_stream(s)
-        outs = []
+        if concurrent_chains:
+            return outs
         for gi, fr in enumerate(fronts):
-            ev = chain_events[gi] if chain_events else None
-            if ev is not None:
-                ev[0].record(main)
+            ev = chain_events[gi]
+            ev[0].record(main)
             U = _native.deflated_polar_chain(fr, hs)
-            if ev is not None:
-                ev[1].record(main)
-            outs.append((U, fr.k, fr.d))
+            ev[1].record(main)
+            outs[gi] = (U, fr.k, fr.d)
         return outs
 
 

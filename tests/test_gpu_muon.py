@@ -181,9 +181,9 @@ def test_cutoff_switches_to_plain_arm(muon_mod, monkeypatch):
 
 @pytest.mark.parametrize("arm", ["deflated_ns_cut", "deflated_pe_cut"])
 def test_polar_groups_equal_per_group_calls(arm):
-    """The concurrent front-ends of polar_groups (one stream per shape group, then
-    the chains in order) give bit-for-bit the per-group polar_group results:
-    polar factors, gate widths k and divisors d."""
+    """polar_groups (one stream per shape group; the chains either on the groups'
+    streams or, with chain events, in turn on the current stream) gives bit for bit
+    the per-group polar_group results: polar factors, gate widths k and divisors d."""
     from defmuon_amd import synthetic as S
     from defmuon_amd.optim import deflation_cutoff as C
     fac = C.ARMS[arm]()
@@ -200,14 +200,17 @@ def test_polar_groups_equal_per_group_calls(arm):
         return out
 
     evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in As]
-    got = fac.polar_groups(As, gens(), steps=5, chain_events=evs)
+    got_seq = fac.polar_groups(As, gens(), steps=5, chain_events=evs)   # chains in turn
+    got = fac.polar_groups(As, gens(), steps=5)                          # chains per stream
     want = [fac.polar_group(A, generator=g, steps=5) for A, g in zip(As, gens())]
     torch.cuda.synchronize()
-    for gi, ((u1, k1, d1), (u2, k2, d2)) in enumerate(zip(got, want)):
-        assert torch.equal(k1, k2), (gi, k1, k2)
-        assert torch.equal(d1, d2), (gi, d1, d2)
-        assert torch.equal(u1.view(torch.int16), u2.view(torch.int16)), gi
-        assert k1.min().item() == 3, (gi, k1)
+    for res in (got_seq, got):
+        for gi, ((u1, k1, d1), (u2, k2, d2)) in enumerate(zip(res, want)):
+            assert torch.equal(k1, k2), (gi, k1, k2)
+            assert torch.equal(d1, d2), (gi, d1, d2)
+            assert torch.equal(u1.view(torch.int16), u2.view(torch.int16)), gi
+            assert k1.min().item() == 3, (gi, k1)
+    for gi in range(len(As)):
         assert evs[gi][0].elapsed_time(evs[gi][1]) > 0.0
 
 
