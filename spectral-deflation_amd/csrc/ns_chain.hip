@@ -197,10 +197,12 @@ __device__ __forceinline__ bf16x8 lds_tr_frag(const char* p) {
 }
 
 // Store 8 consecutive bf16 at dst (elements q with mask bit q set); a full, aligned
-// chunk leaves as one 16-byte store.
+// chunk leaves as one 16-byte non-temporal store: the products are read back only by
+// the next launch, so they should not evict the operand panels this launch's other
+// tiles still read from L2.
 __device__ __forceinline__ void store8(bf16* dst, const bf16x8& v, unsigned mask, bool aligned) {
   if (mask == 0xffu && aligned) {
-    *(bf16x8*)dst = v;
+    __builtin_nontemporal_store(v, (bf16x8*)dst);
   } else {
 #pragma unroll
     for (int q = 0; q < 8; ++q)
