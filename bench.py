@@ -468,10 +468,11 @@ def main():
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                      "traffic": traffic.get("ns_chain_hbm_bytes_per_step"),
-                     "traffic_scope": ("HBM bytes per polar step over the NS chain launches, "
-                                       "measured with rocprofv3 --pmc FETCH_SIZE (x2) and "
-                                       "WRITE_SIZE (x1), scales from torch's copy kernel; "
-                                       + traffic.get("source", "not measured"))
+                     "traffic_scope": ("bytes per polar step the L2 fetched from and wrote to "
+                                       "the memory fabric (MALL or HBM) over the NS chain "
+                                       "launches, measured with rocprofv3 --pmc FETCH_SIZE "
+                                       "(x2) and WRITE_SIZE (x1), scales from torch's copy "
+                                       "kernel; " + traffic.get("source", "not measured"))
                      if traffic else None,
                      "kernel": "NS chain (gemm_nt_bf16 K1/K2/K3 launches of a polar step), "
                                "canonical dense 4m^2n+2m^3 FLOP per matrix-iteration",
