@@ -150,59 +150,6 @@ __global__ __launch_bounds__(256) void skinny_gemm(const float* __restrict__ A, 
 #undef DMH_SG_LOAD
 }
 
-// ---------------------------------------------------------------------------
-// fp64 Gram of a (rows x RP) fp32 matrix, partial over GRAM_CHUNKS row chunks
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gram_partials(const float* __restrict__ Y, int rows,
-                                                     long long y_bs, double* __restrict__ part) {
-  __shared__ float Ys[64 * RP];
-  const int b = blockIdx.y, chunk = blockIdx.x;
-  const int per = (rows + GRAM_CHUNKS - 1) / GRAM_CHUNKS;
-  const int lo = chunk * per, hi = min(rows, lo + per);
-  Y += (long long)b * y_bs;
-  const int tid = threadIdx.x;
-  const int bi = tid >> 4, bj = tid & 15;   // this thread's 4x4 block of the Gram
-  double g[4][4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) g[a][c] = 0.0;
-  // the next 64-row block is loaded into registers while the current one is used
-  float nx[16];
-  auto load = [&](int base) {
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int e = tid + 256 * u;
-      const int row = base + (e >> 6);
-      nx[u] = row < hi ? Y[(long long)row * RP + (e & 63)] : 0.f;
-    }
-  };
-  if (lo < hi) load(lo);
-  for (int base = lo; base < hi; base += 64) {
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 16; ++u) Ys[tid + 256 * u] = nx[u];
-    __syncthreads();
-    if (base + 64 < hi) load(base + 64);
-    const int nr = min(64, hi - base);
-    for (int rr = 0; rr < nr; ++rr) {
-      const float4 x = *(const float4*)&Ys[rr * RP + 4 * bi];
-      const float4 y = *(const float4*)&Ys[rr * RP + 4 * bj];
-      const double xv[4] = {x.x, x.y, x.z, x.w};
-      const double yv[4] = {y.x, y.y, y.z, y.w};
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) g[a][c] = fma(xv[a], yv[c], g[a][c]);
-    }
-  }
-  double* out = part + ((long long)b * GRAM_CHUNKS + chunk) * RP * RP;
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) out[(4 * bi + a) * RP + 4 * bj + c] = g[a][c];
-}
-
 __device__ void sum_gram_partials(const double* part, int b, int r, double (*G)[RP + 1]) {
   const double* p = part + (long long)b * GRAM_CHUNKS * RP * RP;
   for (int e = threadIdx.x; e < RP * RP; e += blockDim.x) {
@@ -483,6 +430,81 @@ __device__ __forceinline__ float4 sk_ld4(__amdgpu_buffer_rsrc_t r, unsigned off)
 __device__ __forceinline__ float2 sk_ld2(__amdgpu_buffer_rsrc_t r, unsigned off) {
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
 }
+// ---------------------------------------------------------------------------
+// fp64 Gram of a (rows x RP) fp32 matrix, partial over GRAM_CHUNKS row chunks: one
+// wave per chunk on the fp64 MFMA (v_mfma_f64_16x16x4_f64, D[i][j] += sum_k A[i][k]
+// B[k][j] over 4 rows k); a second wave per chunk, adding up through LDS, was slower.  Lane l loads row r + l/16, columns 4(l%16) .. +3 (a wave
+// covers 4 whole rows, 1 KB contiguous) and supplies element c of its quad as A[l%16]
+// [l/16] and B[l/16][l%16] of column class c: the product of classes c and c' is the
+// 16 x 16 block G[4i + c][4j + c'].  The ten blocks c <= c' hold every entry of the
+// symmetric Gram once; the store mirrors the off-diagonal classes.  Output element e of
+// lane l is block entry (i, j) = (l/16 + 4e, l%16) (lane layout checked on the device).
+// Products of fp32 values are exact in fp64; only the order of the fp64 sums differs
+// from a row-by-row loop.  Two register sets of GRAM_G 4-row groups alternate, so one
+// set's loads are in flight while the other's MFMAs run (rows at or past the chunk's
+// end load zeros through the buffer descriptor).
+// ---------------------------------------------------------------------------
+constexpr int GRAM_G = 4;   // 4-row groups per register set
+
+__device__ __forceinline__ void gram_mfma(const float4 (&v)[GRAM_G], f64x4 (&acc)[10]) {
+#pragma unroll
+  for (int u = 0; u < GRAM_G; ++u) {
+    const double a[4] = {(double)v[u].x, (double)v[u].y, (double)v[u].z, (double)v[u].w};
+    int t = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int c2 = c; c2 < 4; ++c2, ++t)
+        acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[c], a[c2], acc[t], 0, 0, 0);
+  }
+}
+
+__global__ __launch_bounds__(64) void gram_partials(const float* __restrict__ Y, int rows,
+                                                    long long y_bs, double* __restrict__ part) {
+  const int b = blockIdx.y, chunk = blockIdx.x, l = threadIdx.x;
+  const int per = (rows + GRAM_CHUNKS - 1) / GRAM_CHUNKS;
+  const int lo = chunk * per, hi = min(rows, lo + per);
+  const __amdgpu_buffer_rsrc_t yr = sk_rsrc(Y + (long long)b * y_bs, (long long)rows * RP);
+  const int kr = l >> 4, cq = 4 * (l & 15);
+  auto load = [&](int r0, float4 (&v)[GRAM_G]) {
+#pragma unroll
+    for (int u = 0; u < GRAM_G; ++u) {
+      const int row = r0 + 4 * u + kr;
+      v[u] = sk_ld4(yr, row < hi ? (unsigned)(row * RP + cq) * 4u : SK_OOB);
+    }
+  };
+  f64x4 acc[10];
+#pragma unroll
+  for (int t = 0; t < 10; ++t) acc[t] = f64x4{0.0, 0.0, 0.0, 0.0};
+  constexpr int SET = 4 * GRAM_G;   // rows per register set
+  float4 va[GRAM_G], vb[GRAM_G];
+  load(lo, va);
+  // (the empty asm statements keep each set's loads where they are: hoisted, they would
+  // wait for the other set's loads still in flight)
+  for (int r = lo; r < hi; r += 2 * SET) {
+    load(r + SET, vb);
+    asm volatile("" ::: "memory");
+    gram_mfma(va, acc);
+    asm volatile("" ::: "memory");
+    load(r + 2 * SET, va);
+    asm volatile("" ::: "memory");
+    gram_mfma(vb, acc);
+    asm volatile("" ::: "memory");
+  }
+  double* out = part + ((long long)b * GRAM_CHUNKS + chunk) * RP * RP;
+  int t = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int c2 = c; c2 < 4; ++c2, ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int p = 4 * (kr + 4 * e) + c, q = cq + c2;
+        out[p * RP + q] = acc[t][e];
+        if (c != c2) out[q * RP + p] = acc[t][e];
+      }
+}
+
 // A copy the compiler cannot fold away: a prefetch slot is copied out before its next
 // load is issued into the same registers, so the loop carries the slot in place and no
 // register move of in-flight data (which would wait for the load) is needed at the
@@ -1377,9 +1399,11 @@ static RsvdWs rsvd_layout(void* base, int B, int n, int m) {
 }
 
 static int check_dims(const char* what, int B, int n, int m, int r) {
-  if (B < 0 || n <= 0 || m <= 0 || r <= 0 || r > RP || r > m || n < m) {
-    set_error("%s: unsupported shape (B=%d n=%d m=%d r=%d; need n >= m >= r, 1 <= r <= %d)",
-              what, B, n, m, r, RP);
+  // (the Gram kernel addresses a sketch-width panel, n x RP fp32, with 32-bit offsets)
+  if (B < 0 || n <= 0 || m <= 0 || r <= 0 || r > RP || r > m || n < m ||
+      (long long)n * RP * 4 >= (1LL << 31)) {
+    set_error("%s: unsupported shape (B=%d n=%d m=%d r=%d; need n >= m >= r, 1 <= r <= %d, "
+              "n < 2^23)", what, B, n, m, r, RP);
     return DMH_EINVAL;
   }
   return DMH_OK;
@@ -1402,7 +1426,7 @@ static int sg(hipStream_t st, int mode, const float* A, int B, int n, int m, con
 }
 
 static int gram(hipStream_t st, const float* Y, int B, int rows, double* part) {
-  hipLaunchKernelGGL(gram_partials, dim3(GRAM_CHUNKS, B), dim3(256), 0, st, Y, rows,
+  hipLaunchKernelGGL(gram_partials, dim3(GRAM_CHUNKS, B), dim3(64), 0, st, Y, rows,
                      (long long)rows * RP, part);
   DMH_CHECK_LAUNCH("gram_partials");
   return DMH_OK;
