@@ -167,6 +167,27 @@ def test_zero_matrix_is_declined_and_finite(N):
     assert int(ko[0]) == 2
 
 
+def test_non_finite_matrix_is_isolated(N):
+    """A momentum holding a NaN (undefined in the reference: its NaN sketch reaches
+    cholesky_ex) is declined (k = 0), and every other matrix of the batch comes out
+    bit-identical to a batch without it: no kernel mixes matrices."""
+    from defmuon_amd.optim import deflation_batched as DB
+    fac = DB.DeflatedNSPolar()
+    spec = [((640, 256), dict(seed=70 + i, n_spikes=3, hi=50.0, lo=20.0)) for i in range(3)]
+    A = _spiked_batch(spec)
+    r, kw = O.sketch_dims(256)
+    Om = O.draw_omega(3, 256, r, 21)
+    Ap = A.clone()
+    Ap[1, 17, 5] = float("nan")
+    U0, k0, d0 = fac.polar_group(A.to(DEV), Omega=Om.to(DEV), steps=5)
+    U1, k1, d1 = fac.polar_group(Ap.to(DEV), Omega=Om.to(DEV), steps=5)
+    assert int(k1[1]) == 0 and int(k0[1]) == 3
+    for b in (0, 2):
+        assert int(k1[b]) == int(k0[b]) == 3
+        assert float(d1[b]) == float(d0[b])
+        assert torch.equal(U1[b].view(torch.int16), U0[b].view(torch.int16)), b
+
+
 @pytest.mark.parametrize("arm", ["ns", "pe"])
 def test_fused_deflated_polar_matches_two_calls(N, arm):
     """dmh_deflated_polar (clip written straight into the chain's operands) gives
