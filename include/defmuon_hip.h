@@ -57,7 +57,8 @@ int dmh_ns_chain(dmh_stream_t stream, const void* x, int x_dtype, int batch, int
 
 /* ---- randomized-SVD deflation front-end (fp32, fp64 Gram) --------------------
  * One workspace size serves dmh_orth (call it with n = rows, m = r), dmh_project,
- * dmh_rsvd and dmh_rmfro_clip.
+ * dmh_rsvd and dmh_rmfro_clip.  Shapes: n >= m >= r, 1 <= r <= 64, n < 2^23 rows
+ * (status 1 and "unsupported shape" otherwise).
  */
 int dmh_rsvd_workspace_size(int batch, int n, int m, int r, size_t* bytes);
 int dmh_rmfro_workspace_size(int batch, int n, int m, int r, size_t* bytes);
