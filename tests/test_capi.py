@@ -49,6 +49,10 @@ def test_rsvd_workspace_limits(lib):
     assert lib.dmh_rsvd_workspace_size(3, 5120, 1280, 65, ctypes.byref(n)) == 1
     assert b"unsupported shape" in lib.dmh_last_error()
     assert lib.dmh_rsvd_workspace_size(3, 100, 200, 8, ctypes.byref(n)) == 1   # n < m
+    # sketch-width panels (n x 64 fp32) are addressed with 32-bit offsets: n < 2^23
+    assert lib.dmh_rsvd_workspace_size(1, (1 << 23) - 1, 64, 64, ctypes.byref(n)) == 0
+    assert lib.dmh_rsvd_workspace_size(1, 1 << 23, 64, 64, ctypes.byref(n)) == 1
+    assert b"unsupported shape" in lib.dmh_last_error()
 
 
 def test_entry_points_reject_bad_arguments_without_launching(lib):
