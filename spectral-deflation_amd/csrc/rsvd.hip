@@ -274,13 +274,24 @@ __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restric
 // C (rows x RP) = Y (rows x RP) * M (RP x RP), per matrix; 64 rows per workgroup,
 // a 4 x 4 output block per thread.  CT (optional): the same product transposed,
 // RP x ldct per matrix (the layout the skinny GEMMs read their small operand in).
-__global__ __launch_bounds__(256) void right_mult(const float* __restrict__ Y, int rows,
-                                                  long long y_bs, const float* __restrict__ M,
-                                                  float* __restrict__ C, long long c_bs,
-                                                  float* __restrict__ CT, int ldct) {
+struct RightMult {
+  const float* Y; int rows; long long y_bs;
+  const float* M;
+  float* C; long long c_bs;
+  float* CT; int ldct;
+};
+
+// rows r0 .. r0 + 63 of matrix b
+__device__ __forceinline__ void right_mult_tile(const RightMult& p, int b, int r0) {
+  const float* __restrict__ Y = p.Y;
+  const float* __restrict__ M = p.M;
+  float* __restrict__ C = p.C;
+  float* __restrict__ CT = p.CT;
+  const int rows = p.rows, ldct = p.ldct;
+  const long long y_bs = p.y_bs, c_bs = p.c_bs;
   __shared__ __attribute__((aligned(16))) float Ms[RP * RP];
   __shared__ __attribute__((aligned(16))) float Ys[64][RP + 4];
-  const int b = blockIdx.y, r0 = blockIdx.x * 64, tid = threadIdx.x;
+  const int tid = threadIdx.x;
   const float* Mb = M + (long long)b * RP * RP;
   const float* Yb = Y + (long long)b * y_bs;
 #pragma unroll
@@ -329,6 +340,19 @@ __global__ __launch_bounds__(256) void right_mult(const float* __restrict__ Y, i
         if (row0 + i < rows) dst[i] = acc[i][k];
     }
   }
+}
+
+// grid (ceil(rows / 64), batch)
+__global__ __launch_bounds__(256) void right_mult(RightMult p) {
+  right_mult_tile(p, blockIdx.y, blockIdx.x * 64);
+}
+
+// two independent products in one launch (U = Q Ub and V = Bp^T Ub diag(1/s) of the
+// Rayleigh-Ritz step): grid (ceil(p.rows / 64) + ceil(q.rows / 64), batch)
+__global__ __launch_bounds__(256) void right_mult_pair(RightMult p, RightMult q) {
+  const int np = (p.rows + 63) / 64;
+  if ((int)blockIdx.x < np) right_mult_tile(p, blockIdx.y, blockIdx.x * 64);
+  else right_mult_tile(q, blockIdx.y, (blockIdx.x - np) * 64);
 }
 
 // dst (RP x ldd per matrix) = src^T for src (rows x cols, leading dim lds), zero
@@ -1444,9 +1468,9 @@ static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int
     if ((rc = gram(st, src, B, rows, w.gram))) return rc;
     hipLaunchKernelGGL(chol_inv, dim3(B), dim3(CHOL_THREADS), 0, st, w.gram, r, w.M, w.degen);
     DMH_CHECK_LAUNCH("chol_inv");
-    hipLaunchKernelGGL(right_mult, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, src, rows,
-                       (long long)rows * RP, w.M, dst, (long long)rows * RP,
-                       last ? QT : (float*)nullptr, rows);
+    const RightMult rm{src, rows, (long long)rows * RP, w.M, dst, (long long)rows * RP,
+                       last ? QT : (float*)nullptr, rows};
+    hipLaunchKernelGGL(right_mult, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, rm);
     DMH_CHECK_LAUNCH("right_mult");
     src = dst;
   }
@@ -1483,6 +1507,16 @@ static int skc(hipStream_t st, const float* A, int B, int n, int m, const float*
   hipLaunchKernelGGL(sk_reduce, dim3((unsigned)ceil_div(per / 4, 256)), dim3(256), 0, st, w.part,
                      S, per, C);
   DMH_CHECK_LAUNCH("sk_reduce");
+  return DMH_OK;
+}
+
+// U = Q Ub and V = Bp^T Ub diag(1/s), one launch
+static int launch_uv(hipStream_t st, const RsvdWs& w, int B, int n, int m) {
+  const RightMult pu{w.Q, n, (long long)n * RP, w.Ub, w.U, (long long)n * RP, nullptr, 0};
+  const RightMult pv{w.Bt, m, (long long)m * RP, w.UbS, w.V, (long long)m * RP, nullptr, 0};
+  hipLaunchKernelGGL(right_mult_pair, dim3(ceil_div(n, 64) + ceil_div(m, 64), B), dim3(256), 0,
+                     st, pu, pv);
+  DMH_CHECK_LAUNCH("right_mult (U, V)");
   return DMH_OK;
 }
 
@@ -1538,13 +1572,7 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
                      d ? w.asq : nullptr, ceil_div(n, fast ? SKR_ROWS : SG_ROWS), d);
   DMH_CHECK_LAUNCH("eig_gate");
   // U = Q Ub ; V = Bp^T Ub diag(1/s)
-  hipLaunchKernelGGL(right_mult, dim3(ceil_div(n, 64), B), dim3(256), 0, st, w.Q, n,
-                     (long long)n * RP, w.Ub, w.U, (long long)n * RP, (float*)nullptr, 0);
-  DMH_CHECK_LAUNCH("right_mult (U)");
-  hipLaunchKernelGGL(right_mult, dim3(ceil_div(m, 64), B), dim3(256), 0, st, w.Bt, m,
-                     (long long)m * RP, w.UbS, w.V, (long long)m * RP, (float*)nullptr, 0);
-  DMH_CHECK_LAUNCH("right_mult (V)");
-  return DMH_OK;
+  return launch_uv(st, w, B, n, m);
 }
 
 static int launch_restore(hipStream_t st, const float* A, int B, int n, int m, const RsvdWs& w,
@@ -1655,11 +1683,7 @@ int dmh_project(hipStream_t stream, const float* Q, const float* A, int batch, i
                      w.Ub, w.UbS, w.k64, w.kint, w.cw, w.cr, (const double*)nullptr,
                      (const double*)nullptr, 0, (float*)nullptr);
   DMH_CHECK_LAUNCH("eig_gate");
-  hipLaunchKernelGGL(right_mult, dim3(ceil_div(n, 64), batch), dim3(256), 0, stream, w.Q, n,
-                     (long long)n * RP, w.Ub, w.U, (long long)n * RP, (float*)nullptr, 0);
-  hipLaunchKernelGGL(right_mult, dim3(ceil_div(m, 64), batch), dim3(256), 0, stream, w.Bt, m,
-                     (long long)m * RP, w.UbS, w.V, (long long)m * RP, (float*)nullptr, 0);
-  DMH_CHECK_LAUNCH("right_mult (U, V)");
+  if ((rc = launch_uv(stream, w, batch, n, m))) return rc;
   return copy_usv(stream, w, batch, n, m, r, U, s, V);
 }
 
