@@ -1,4 +1,4 @@
-"""GPU parity at the full BASELINE.json shapes of configs 3 and 4.
+"""GPU parity at the full BASELINE.json shapes of configs 3, 4 and 5.
 
 Config 3: GPT-2 small, one Muon polar step per arm over 48 x (768, 768) and
 24 x (3072, 768) tall matrices (12 layers x {3 QKV blocks, attn proj} and
@@ -6,6 +6,8 @@ Config 3: GPT-2 small, one Muon polar step per arm over 48 x (768, 768) and
 Config 4: GPT-2 medium, deflated_pe_cut over 96 x (1024, 1024) and
 48 x (4096, 1024), 16 spikes 100x..5x (expected k = 12) with every 4th matrix
 left unspiked (expected k = 0).
+Config 5: GPT-2 large, deflated_ns_cut over 144 x (1280, 1280) and 72 x (5120, 1280)
+(the bench workload), 8 spikes 50x..10x (expected k = 8).
 
 Every gate decision is checked exactly; the polar factors are checked against
 the oracle (same sketch, drawn with the reference's seed formula, muon.py:290-291)
@@ -23,6 +25,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 SMALL = [(48, 768, 768), (24, 3072, 768)]
 MEDIUM = [(96, 1024, 1024), (48, 4096, 1024)]
+LARGE = [(144, 1280, 1280), (72, 5120, 1280)]
 
 
 @pytest.fixture(scope="module")
@@ -108,3 +111,18 @@ def test_config4_gpt2_medium_pe(mods):
         assert k.tolist() == want, k.tolist()
         assert torch.isfinite(U.float()).all()
         _check_deflated_sample("deflated_pe_cut", A, Om, U, [0, 1])
+
+
+def test_config5_gpt2_large_deflated(mods):
+    """The bench workload itself: every gate fires with k = 8, and the first and last
+    matrix of each group match the oracle on their own sketches."""
+    S, C, _, _ = mods
+    for gi, (B, n, m) in enumerate(LARGE):
+        A = S.spiked_batch(B, n, m, seed=500 + gi, n_spikes=8, hi=50.0, lo=10.0, device=DEV)
+        U, k, Om = _deflated_group(C, "deflated_ns_cut", A, gi)
+        assert S.expected_k(8, 50.0, 10.0) == 8
+        assert k.tolist() == [8] * B, k.tolist()
+        assert torch.isfinite(U.float()).all()
+        _check_deflated_sample("deflated_ns_cut", A, Om, U, [0, B - 1])
+        del A, U, Om
+        torch.cuda.empty_cache()
