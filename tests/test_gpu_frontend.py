@@ -167,6 +167,25 @@ def test_zero_matrix_is_declined_and_finite(N):
     assert int(ko[0]) == 2
 
 
+def test_empty_group(N):
+    """An empty shape group (batch 0): every entry returns empty outputs of the right
+    shapes without launching anything."""
+    from defmuon_amd.optim import deflation_batched as DB
+    A = torch.empty(0, 512, 256, device=DEV)
+    r, kw = O.sketch_dims(256)
+    Om = torch.empty(0, 256, r, device=DEV)
+    X0, k, d = N.rmfro_clip(A, Om, kw, O.GATE_RATIO, O.DEFLATE_THRESH, O.DIVISOR_PAD, 1, 1,
+                            torch.bfloat16)
+    assert X0.shape == (0, 512, 256) and k.shape == (0,) and d.shape == (0,)
+    U, s, V = N.rsvd(A, Om, 1, 1)
+    assert U.shape[0] == s.shape[0] == V.shape[0] == 0
+    P, k2, d2 = DB.DeflatedNSPolar().polar_group(A, Omega=Om, steps=5)
+    assert P.shape == (0, 512, 256) and P.dtype == torch.bfloat16 and k2.numel() == 0
+    Y = N.ns_chain(torch.empty(0, 300, 200, device=DEV), True, 1, [O.NS_ABC] * 5)
+    assert Y.shape == (0, 300, 200)
+    torch.cuda.synchronize()
+
+
 def test_non_finite_matrix_is_isolated(N):
     """A momentum holding a NaN (undefined in the reference: its NaN sketch reaches
     cholesky_ex) is declined (k = 0), and every other matrix of the batch comes out
