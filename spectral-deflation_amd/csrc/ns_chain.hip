@@ -350,6 +350,7 @@ void gemm_nt_bf16(GemmArgs g) {
   f32x16 acc[BM][BN];
   bf16x8 f0p[BM], f0q[BN], f1p[BM], f1q[BN];
   int s_cur = 0;   // ring slot of the stage being consumed
+  int vm_after = 0; // vector memory instructions issued after the prefetch of stage 0
   for (;;) {
     // the workgroup's next tile, if any (its first stages are loaded and prefetched
     // during this tile's last steps)
@@ -366,9 +367,20 @@ void gemm_nt_bf16(GemmArgs g) {
     //    substep 0 of stage kt+1 under the last substep of stage kt, so the MFMA pipe
     //    never waits on LDS; the one barrier per stage sits before the last substep.
     // The slot refilled at step kt (stage kt+1) held stage kt-1, whose last fragment
-    // reads completed (lgkmcnt(0)) before the barrier of step kt-1.  The wait for
-    // stage 0 also covers the previous tile's epilogue stores (vmcnt counts both).
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // reads completed (lgkmcnt(0)) before the barrier of step kt-1.
+    // Stage 0 was requested before the previous tile's epilogue, whose vm_after
+    // vector memory instructions (aux loads, stores) followed it.  Vector memory
+    // instructions of a wave complete in order (the compiler's own waits in the
+    // epilogue count on it too), so waiting until at most vm_after are outstanding
+    // lands stage 0 and leaves the stores draining under this tile's first stage.
+    // (the builtin, not inline asm, so that the compiler's own wait tracking sees it;
+    // encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
+    switch (vm_after) {
+      case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
+      case 32: __builtin_amdgcn_s_waitcnt(0x8F70); break;
+      case 48: __builtin_amdgcn_s_waitcnt(0xCF70); break;
+      default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
     ring_barrier();
 #pragma unroll
     for (int i = 0; i < BM; ++i)
@@ -431,31 +443,40 @@ void gemm_nt_bf16(GemmArgs g) {
     __builtin_amdgcn_s_setprio(0);
 
     // ---- epilogue (per wave, no workgroup barrier) ----------------------------
-    // The wave's 128 x 64 output goes out one 32 x 64 block row at a time through
-    // its 4 KB staging area:
-    //   phase 1  acc -> staging: v = bf16(acc) (bf16(c * acc) for POLY)
-    //   phase 2  row-major pass, 16-byte chunks: POLY epilogue (aux read in 16 B,
-    //            written back for phase 3), store C[i][j]
-    //   phase 3  transposed pass: 8 rows x 4 columns per lane, transposed in
-    //            registers, store C^T[j][i] in 16-byte chunks
-    // Staging element (r, c) sits at byte r*128 + 16*((c>>3) ^ (r&7)) + 2*(c&7): the
-    // accesses of all three phases spread over every bank.  acc[i][j][4g+q] holds
-    // C[32 i + (lane&31)][32 j + 8g + 4(lane>>5) + q] of the wave tile.
-    // Symmetric products (upper tiles only): off-diagonal tiles store both C and
-    // C^T; on a diagonal tile only the elements with i <= j are stored, once
-    // row-major and once transposed, so the lower triangle takes the upper one's
-    // values exactly.
+    // The wave's 128 x 64 output goes out through its 4 KB staging area:
+    //   row pass, one 32 x 64 block row at a time:
+    //     phase 1  acc -> staging: v = bf16(acc) (bf16(c * acc) for POLY)
+    //     phase 2  16-byte chunks: POLY epilogue (aux read in 16 B), store C[i][j];
+    //              with a transposed store to come, POLY's values go back into acc
+    //              (phase 2b, through the staging area)
+    //   transposed pass (outT), one 64 x 32 block at a time: acc -> staging, then
+    //     each lane reads 8 rows x 4 columns, transposes them in registers and
+    //     stores C^T[j][i] in 16-byte chunks; the 64 lanes of a store cover 8 whole
+    //     128-byte lines (8 rows j x 64 i).  (Half-line stores of a transposed
+    //     32-row block made the next launch's reads of those lines slow: the chain
+    //     ran 10% longer.)
+    // Row-pass staging element (r, c) sits at byte r*128 + 16*((c>>3) ^ (r&7)) +
+    // 2*(c&7); transposed-pass element (i, j) at i*64 + 8*((j>>2) ^ (i&7)) + 2*(j&3).
+    // acc[i][j][4g+q] holds C[32 i + (lane&31)][32 j + 8g + 4(lane>>5) + q] of the
+    // wave tile.
+    // Diagonal tiles of a symmetric product are stored whole, row-major: the MFMAs
+    // compute C[i][j] and C[j][i] from the same products in the same order.
     {
       const int wi0 = ti * TILE + WT_M * wm, wj0 = tj * TILE + WT_N * wn;
       const bool diag = g.sym && ti == tj;
       bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
-      bf16* outtb = g.outT ? g.outT + (long long)b * g.outT_bs : nullptr;
+      bf16* outtb = g.outT && !diag ? g.outT + (long long)b * g.outT_bs : nullptr;
       const bool al_out = (g.out_ld & 7) == 0, al_outT = (g.outT_ld & 7) == 0;
       const bf16* auxb = EPI == EPI_POLY ? g.aux + (long long)b * g.aux_bs : nullptr;
+      // one store per 16-byte chunk when the wave's 128 x 64 block is whole and
+      // aligned: the epilogue then issues a known number of memory instructions
+      const bool whole = wi0 + WT_M <= g.valid_i && wj0 + WT_N <= g.valid_j &&
+                         (!outb || al_out) && (!outtb || al_outT);
+      vm_after = whole ? (outb ? 16 : 0) + (outtb ? 16 : 0) + (EPI == EPI_POLY ? 16 : 0) : -1;
       // POLY: the aux of block rows 0 and 1 is requested up front and that of row
       // bi+2 once row bi's accumulators are drained, so the reads run two block rows
       // ahead of their use (latency hidden, registers bounded)
-      constexpr int AUX_AHEAD = 2;
+      constexpr int AUX_AHEAD = 1;
       bf16x8 av[EPI == EPI_POLY ? BM : 1][4];
       auto load_aux = [&](int bi) {
 #pragma unroll
@@ -507,47 +528,70 @@ void gemm_nt_bf16(GemmArgs g) {
           if (outb && gi < g.valid_i) {
             unsigned mask = 0xffu;
             if (gj + 8 > g.valid_j) mask = gj >= g.valid_j ? 0u : (1u << (g.valid_j - gj)) - 1u;
-            if (diag) {   // keep j >= i
-              const int d = gi - gj;   // elements q >= d
-              mask &= d <= 0 ? 0xffu : (d >= 8 ? 0u : (0xffu << d) & 0xffu);
-            }
             if (mask) store8(outb + (long long)gi * g.out_ld + gj, val, mask, al_out);
           }
         }
-        // phase 3
-        if (outtb) {
-          const int a = lane & 3, c = lane >> 2;   // rows 8a..8a+7, columns 4c..4c+3
-          uint2 rr[8];
+        // phase 2b: POLY's stored values back into acc (the inverse of phase 1)
+        if (EPI == EPI_POLY && outtb) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const int r = 8 * a + q;
-            rr[q] = *(const uint2*)(stg + r * 128 + 16 * ((c >> 1) ^ (r & 7)) + 8 * (c & 1));
+          for (int bj = 0; bj < BN; ++bj) {
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const int ch = 4 * bj + gq;
+              const bf16x4 o = *(const bf16x4*)(stg + r32 * 128 + 16 * (ch ^ (r32 & 7)) + 8 * hi);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[bi][bj][4 * gq + q] = bf2f(o[q]);
+            }
           }
-          const int gi = i0 + 8 * a;
+        }
+      }
+      // transposed pass
+      if (outtb) {
+        const int a = lane & 7, c = lane >> 3;   // rows 8a..8a+7, columns 4c..4c+3 of a block
 #pragma unroll
-          for (int cc = 0; cc < 4; ++cc) {
-            const int gj = wj0 + 4 * c + cc;
-            // column cc of the 8x4 block: halves (cc&1) of words (cc>>1)
-            uint32_t w[4];
+        for (int bp = 0; bp < BM / 2; ++bp) {
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-              const uint32_t x0 = (cc >> 1) ? rr[2 * h].y : rr[2 * h].x;
-              const uint32_t x1 = (cc >> 1) ? rr[2 * h + 1].y : rr[2 * h + 1].x;
-              const uint32_t lo = (cc & 1) ? (x0 >> 16) : (x0 & 0xffffu);
-              const uint32_t hw = (cc & 1) ? (x1 & 0xffff0000u) : (x1 << 16);
-              w[h] = lo | hw;
+          for (int bj = 0; bj < BN; ++bj) {
+            // acc -> staging: block rows 2 bp, 2 bp + 1 (i < 64), column block bj (j < 32)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+              for (int gq = 0; gq < 4; ++gq) {
+                bf16x4 o;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[q] = f2bf(acc[2 * bp + h][bj][4 * gq + q]);
+                const int i = 32 * h + r32, unit = 2 * gq + hi;
+                *(bf16x4*)(stg + i * 64 + 8 * (unit ^ (i & 7))) = o;
+              }
             }
-            if (gj >= g.valid_j) continue;
-            unsigned mask = 0xffu;
-            if (gi + 8 > g.valid_i) mask = gi >= g.valid_i ? 0u : (1u << (g.valid_i - gi)) - 1u;
-            if (diag) {   // keep i <= j
-              const int d = gj - gi;   // elements q <= d
-              mask &= d < 0 ? 0u : (d >= 7 ? 0xffu : (1u << (d + 1)) - 1u);
+            uint2 rr[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const int i = 8 * a + q;
+              rr[q] = *(const uint2*)(stg + i * 64 + 8 * (c ^ q));
             }
-            if (mask) {
-              const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
-              store8(outtb + (long long)gj * g.outT_ld + gi, __builtin_bit_cast(bf16x8, wv), mask,
-                     al_outT);
+            const int gi = wi0 + 64 * bp + 8 * a;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+              const int gj = wj0 + 32 * bj + 4 * c + cc;
+              // column cc of the 8x4 block: halves (cc&1) of words (cc>>1)
+              uint32_t w[4];
+#pragma unroll
+              for (int h = 0; h < 4; ++h) {
+                const uint32_t x0 = (cc >> 1) ? rr[2 * h].y : rr[2 * h].x;
+                const uint32_t x1 = (cc >> 1) ? rr[2 * h + 1].y : rr[2 * h + 1].x;
+                const uint32_t lo = (cc & 1) ? (x0 >> 16) : (x0 & 0xffffu);
+                const uint32_t hw = (cc & 1) ? (x1 & 0xffff0000u) : (x1 << 16);
+                w[h] = lo | hw;
+              }
+              if (gj >= g.valid_j) continue;
+              unsigned mask = 0xffu;
+              if (gi + 8 > g.valid_i) mask = gi >= g.valid_i ? 0u : (1u << (g.valid_i - gi)) - 1u;
+              if (mask) {
+                const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
+                store8(outtb + (long long)gj * g.outT_ld + gi, __builtin_bit_cast(bf16x8, wv), mask,
+                       al_outT);
+              }
             }
           }
         }
