@@ -55,6 +55,19 @@ int dmh_ns_chain(dmh_stream_t stream, const void* x, int x_dtype, int batch, int
                  int orient_tall, int entry_mode, const double* coeffs, int steps, void* ws,
                  size_t ws_bytes);
 
+/* Allocation-free variant of dmh_ns_chain.  It has no counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments
+ * without the workspace, which is a static device array of DMH_NS_SCRATCH_BYTES
+ * (64 MiB) per GPU, held from the first call on that GPU until the process ends.
+ * A shape whose workspace (dmh_ns_workspace_size) exceeds it returns 2.  Every call
+ * on one GPU uses the same array: calls that overlap on one GPU race. */
+#define DMH_NS_SCRATCH_BYTES (64u << 20)
+int dmh_ns_chain_noalloc(dmh_stream_t stream, const void* x, int x_dtype, int batch, int rows,
+                         int cols, long long x_bstride, long long x_rstride,
+                         long long x_cstride, void* out, int orient_tall, int entry_mode,
+                         const double* coeffs, int steps);
+
 /* ---- randomized-SVD deflation front-end (fp32, fp64 Gram) --------------------
  * One workspace size serves dmh_orth (call it with n = rows, m = r), dmh_project,
  * dmh_rsvd and dmh_rmfro_clip.  Shapes: n >= m >= r, 1 <= r <= 64, n < 2^23 rows

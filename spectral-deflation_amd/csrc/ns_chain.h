@@ -8,6 +8,10 @@ namespace dmh {
 
 constexpr int CHAIN_TILE = 256;
 
+// size of the static workspace of dmh_ns_chain_noalloc (the same value as
+// DMH_NS_SCRATCH_BYTES in include/defmuon_hip.h)
+#define DMH_NS_SCRATCH_BYTES (64u << 20)
+
 struct ChainDims {
   int n, m, np, mp;   // tall operand T is n x m; padded to multiples of CHAIN_TILE
 };

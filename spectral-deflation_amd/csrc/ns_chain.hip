@@ -32,6 +32,7 @@
 #include "common.h"
 #include "ns_chain.h"
 
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -875,3 +876,67 @@ int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int 
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// dmh_ns_chain_noalloc: dmh_ns_chain with its workspace in a static device array
+// (for callers that cannot allocate: code under HIP graph capture, serving loops,
+// harnesses that forbid hipMalloc).  Each GPU holds its own copy of the array from
+// the first call on it until the process ends.  The array's host-side name is not a
+// device address: its address on the current device comes from hipGetSymbolAddress,
+// once per device, and only that pointer is handed to kernels.  Every call on a GPU
+// uses the same array, so calls that overlap on one GPU (other streams, other
+// threads) race; the chain writes every byte of its workspace it reads, so nothing
+// needs clearing between calls.
+// ---------------------------------------------------------------------------
+namespace dmh {
+
+static __device__ __align__(256) unsigned char scratch[DMH_NS_SCRATCH_BYTES];
+
+static int scratch_address(void** out) {
+  constexpr int MAXDEV = 64;
+  static void* addr[MAXDEV];
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) {
+    set_error("dmh_ns_chain_noalloc: no usable current device (%d)", dev);
+    return DMH_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("dmh_ns_chain_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(e));
+      return DMH_ELAUNCH;
+    }
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return DMH_OK;
+}
+
+}  // namespace dmh
+
+extern "C" int dmh_ns_chain_noalloc(hipStream_t stream, const void* x, int x_dtype, int batch,
+                                    int rows, int cols, long long x_bstride, long long x_rstride,
+                                    long long x_cstride, void* out, int orient_tall,
+                                    int entry_mode, const double* coeffs, int steps) {
+  if (batch == 0) return DMH_OK;
+  if (batch < 0 || rows <= 0 || cols <= 0) {
+    set_error("dmh_ns_chain_noalloc: bad arguments (batch=%d rows=%d cols=%d)", batch, rows, cols);
+    return DMH_EINVAL;
+  }
+  const size_t need = chain_ws(nullptr, batch, chain_dims(rows, cols, orient_tall)).bytes;
+  if (need > (size_t)DMH_NS_SCRATCH_BYTES) {
+    set_error("dmh_ns_chain_noalloc: batch=%d of %dx%d needs %zu bytes of workspace, more than "
+              "the %zu-byte static scratch; use dmh_ns_chain with a caller workspace",
+              batch, rows, cols, need, (size_t)DMH_NS_SCRATCH_BYTES);
+    return DMH_EWORKSPACE;
+  }
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return dmh_ns_chain(stream, x, x_dtype, batch, rows, cols, x_bstride, x_rstride, x_cstride, out,
+                      orient_tall, entry_mode, coeffs, steps, ws, (size_t)DMH_NS_SCRATCH_BYTES);
+}

@@ -27,6 +27,9 @@ _SIGS = {
     "dmh_ns_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
     "dmh_ns_chain": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_ll, c_vp,
                              c_int, c_int, ctypes.POINTER(ctypes.c_double), c_int, c_vp, c_sz]),
+    "dmh_ns_chain_noalloc": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_ll,
+                                     c_vp, c_int, c_int, ctypes.POINTER(ctypes.c_double),
+                                     c_int]),
     "dmh_rsvd_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
     "dmh_rmfro_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
     "dmh_orth": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_sz]),
