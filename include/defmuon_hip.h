@@ -68,6 +68,15 @@ int dmh_ns_chain_noalloc(dmh_stream_t stream, const void* x, int x_dtype, int ba
                          long long x_cstride, void* out, int orient_tall, int entry_mode,
                          const double* coeffs, int steps);
 
+/* ---- fp32 tall-convention chain ---------------------------------------------
+ * The dtype-preserving path of _horner_iterate (defmuon/optim/deflation_batched.py:
+ * 196-204) for fp32 input: per (a, b, c) in coeffs, G = X^T X, B = b G + (c G) G,
+ * X <- a X + X B, in fp32.  x, out: (batch, n, m) fp32, contiguous, distinct.
+ */
+int dmh_horner_f32_workspace_size(int batch, int n, int m, size_t* bytes);
+int dmh_horner_f32(dmh_stream_t stream, const float* x, int batch, int n, int m, float* out,
+                   const double* coeffs, int steps, void* ws, size_t ws_bytes);
+
 /* ---- randomized-SVD deflation front-end (fp32, fp64 Gram) --------------------
  * One workspace size serves dmh_orth (call it with n = rows, m = r), dmh_project,
  * dmh_rsvd and dmh_rmfro_clip.  Shapes: n >= m >= r, 1 <= r <= 64, n < 2^23 rows

@@ -922,7 +922,8 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
                                                        float* __restrict__ cr,
                                                        const double* __restrict__ qpart,
                                                        const double* __restrict__ asq, int asq_n,
-                                                       float* __restrict__ d_out) {
+                                                       float* __restrict__ d_out,
+                                                       int* __restrict__ wflag) {
   __shared__ __attribute__((aligned(16))) double Hs[2][RP * JP];   // upper triangle in use
   // per wave: c, s, tan of pair t in slot t (slots 32.. take the duplicates of lanes 32..)
   __shared__ __attribute__((aligned(16))) double ang[EG_WAVES][64][4];
@@ -1176,6 +1177,11 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
     w2 = asum - head;
   }
   if (l == 0) d_out[b] = (float)sqrt(w2 > 0.0 ? w2 : 0.0) + 1e-7f;
+  // When the removed head holds nearly all of A's energy the difference above loses
+  // its digits (its error grows as ||A||^2 / ||W||^2, while an explicit ||W||_F's
+  // grows as ||A|| / ||W||): below 1% of ||A||^2 the matrix is flagged and d is
+  // recomputed from W itself (w_norm_partials, then deflate_restore).
+  if (l == 0 && wflag) wflag[b] = fired && w2 < 1e-2 * asum ? 1 : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1190,6 +1196,11 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
 constexpr int DR_ROWS = 64, DR_COLS = 128;
 constexpr int DR_KC = 16;   // head columns staged per chunk
 
+// restore tiles per matrix (also the count of w_norm_partials' partials)
+__host__ __device__ inline int wn_tiles(int n, int m) {
+  return ((m + DR_COLS - 1) / DR_COLS) * ((n + DR_ROWS - 1) / DR_ROWS);
+}
+
 // LDS of one restore tile: the head chunk (U rows of the tile, V rows of the tile
 // transposed) while the rank-k update runs, then the bf16 tile of W = T^T.
 union RestoreLds {
@@ -1203,7 +1214,8 @@ union RestoreLds {
 __global__ __launch_bounds__(256) void deflate_restore(
     const float* __restrict__ A, int n, int m, const float* __restrict__ U,
     const float* __restrict__ V, const int* __restrict__ kvec, const float* __restrict__ cw,
-    const float* __restrict__ cr, const float* __restrict__ dvec, void* __restrict__ X0,
+    const float* __restrict__ cr, float* __restrict__ dvec, const int* __restrict__ wflag,
+    const double* __restrict__ wpart, void* __restrict__ X0,
     int x0_mode /*0 none, 1 bf16, 2 fp32*/, bf16* __restrict__ T, bf16* __restrict__ W, int np,
     int mp) {
   __shared__ __attribute__((aligned(16))) RestoreLds sm;
@@ -1212,7 +1224,23 @@ __global__ __launch_bounds__(256) void deflate_restore(
   const int i0 = blockIdx.y * DR_ROWS, j0 = blockIdx.x * DR_COLS;
   const int tid = threadIdx.x;
   const int k = kvec[b];
-  const float d = dvec[b];
+  float d = dvec[b];
+  if (wflag && wflag[b]) {
+    // d from W itself: every workgroup sums the same partials in the same order
+    // (so all agree on d bit for bit); the first stores it as the API's d
+    const int nt = wn_tiles(n, m);
+    __shared__ double wsum[256];
+    double acc = 0.0;
+    for (int t = tid; t < nt; t += 256) acc += wpart[(long long)b * nt + t];
+    wsum[tid] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+      if (tid < w) wsum[tid] += wsum[tid + w];
+      __syncthreads();
+    }
+    d = (float)sqrt(wsum[0]) + 1e-7f;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) dvec[b] = d;
+  }
   const float* Ab = A + (long long)b * n * m;
   const int c4 = (tid & 31) * 4;      // 4 consecutive columns of the tile
   const int rw = tid >> 5;            // rows rw + 8a, a = 0..7
@@ -1304,6 +1332,75 @@ __global__ __launch_bounds__(256) void deflate_restore(
   }
 }
 
+// Explicit ||W||_F^2 for the matrices eig_gate flagged (head energy above 99% of
+// ||A||^2): W = A - U diag(cw) V^T over the restore's 64 x 128 tiles, per-thread
+// squares summed in fp64, one partial per tile (wpart[b][tile]); other matrices'
+// workgroups return at once.  deflate_restore turns the partials into d.
+__global__ __launch_bounds__(256) void w_norm_partials(
+    const float* __restrict__ A, int n, int m, const float* __restrict__ U,
+    const float* __restrict__ V, const int* __restrict__ kvec, const float* __restrict__ cw,
+    const int* __restrict__ wflag, double* __restrict__ wpart) {
+  const int b = blockIdx.z;
+  if (!wflag[b]) return;   // uniform over the workgroup
+  __shared__ __attribute__((aligned(16))) RestoreLds sm;
+  __shared__ float coef[RP];
+  __shared__ double red[256];
+  const int i0 = blockIdx.y * DR_ROWS, j0 = blockIdx.x * DR_COLS;
+  const int tid = threadIdx.x;
+  const int k = kvec[b];
+  const float* Ab = A + (long long)b * n * m;
+  const int c4 = (tid & 31) * 4, rw = tid >> 5;
+  float x[8][4];
+#pragma unroll
+  for (int a = 0; a < 8; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
+      x[a][c] = (gi < n && gj < m) ? Ab[(long long)gi * m + gj] : 0.f;
+    }
+  if (tid < RP) coef[tid] = cw[b * RP + tid];
+  for (int t0 = 0; t0 < k; t0 += DR_KC) {
+    const int kc = min(DR_KC, k - t0);
+    __syncthreads();
+    for (int e = tid; e < DR_ROWS * DR_KC; e += 256) {
+      const int rr = e / DR_KC, t = e % DR_KC, gi = i0 + rr;
+      sm.head.Us[rr][t] = (t < kc && gi < n) ? U[((long long)b * n + gi) * RP + t0 + t] : 0.f;
+    }
+    for (int e = tid; e < DR_COLS * DR_KC; e += 256) {
+      const int cc = e / DR_KC, t = e % DR_KC, gj = j0 + cc;
+      sm.head.Vt[t][cc] = (t < kc && gj < m) ? V[((long long)b * m + gj) * RP + t0 + t] : 0.f;
+    }
+    __syncthreads();
+    for (int t = 0; t < kc; ++t) {
+      const float4 v = *(const float4*)&sm.head.Vt[t][c4];
+      const float ct = coef[t0 + t];
+#pragma unroll
+      for (int a = 0; a < 8; ++a) {
+        const float u = sm.head.Us[rw + 8 * a][t] * ct;
+        x[a][0] = fmaf(-u, v.x, x[a][0]);
+        x[a][1] = fmaf(-u, v.y, x[a][1]);
+        x[a][2] = fmaf(-u, v.z, x[a][2]);
+        x[a][3] = fmaf(-u, v.w, x[a][3]);
+      }
+    }
+  }
+  double sq = 0.0;
+#pragma unroll
+  for (int a = 0; a < 8; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
+      if (gi < n && gj < m) sq += (double)x[a][c] * (double)x[a][c];
+    }
+  red[tid] = sq;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) wpart[(long long)b * wn_tiles(n, m) + blockIdx.y * gridDim.x + blockIdx.x] = red[0];
+}
+
 // strided copy of the first r of RP columns: dst (B, rows, r) contiguous
 __global__ __launch_bounds__(256) void copy_cols(const float* __restrict__ src, int rows, int r,
                                                  float* __restrict__ dst) {
@@ -1339,9 +1436,9 @@ __global__ __launch_bounds__(256) void fill_zero_i32(int* __restrict__ p, int co
 struct RsvdWs {
   float *Y, *Q, *Z, *Zq, *Bt, *U, *V, *M, *Ub, *UbS, *cw, *cr, *s;
   float *XT, *QT, *part;   // split-bf16 skinny GEMMs: transposed small operands, row-split partials
-  double *gram, *gramq, *asq;
+  double *gram, *gramq, *asq, *wpart;   // wpart: per-tile sums of W^2 (flagged matrices)
   long long* k64;
-  int *kint, *degen;
+  int *kint, *degen, *wflag;
   size_t bytes;
 };
 
@@ -1411,6 +1508,8 @@ static RsvdWs rsvd_layout(void* base, int B, int n, int m) {
   w.k64 = (long long*)take((size_t)B * sizeof(long long));
   w.kint = (int*)take((size_t)B * sizeof(int));
   w.degen = (int*)take((size_t)B * sizeof(int));
+  w.wflag = (int*)take((size_t)B * sizeof(int));
+  w.wpart = (double*)take((size_t)B * wn_tiles(n, m) * sizeof(double));
   if (sk_fast(n, m)) {
     int S, rps;
     sk_splits(B, n, m, &S, &rps);
@@ -1569,19 +1668,23 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
   if (d && (rc = gram(st, w.Q, B, n, w.gramq))) return rc;
   hipLaunchKernelGGL(eig_gate, dim3(B), dim3(EG_THREADS), 0, st, w.gram, gp, w.degen, w.s, RP, w.Ub,
                      w.UbS, k_out, w.kint, w.cw, w.cr, d ? w.gramq : nullptr,
-                     d ? w.asq : nullptr, ceil_div(n, fast ? SKR_ROWS : SG_ROWS), d);
+                     d ? w.asq : nullptr, ceil_div(n, fast ? SKR_ROWS : SG_ROWS), d,
+                     d ? w.wflag : nullptr);
   DMH_CHECK_LAUNCH("eig_gate");
   // U = Q Ub ; V = Bp^T Ub diag(1/s)
   return launch_uv(st, w, B, n, m);
 }
 
 static int launch_restore(hipStream_t st, const float* A, int B, int n, int m, const RsvdWs& w,
-                          const float* d, void* X0, int x0_mode, bf16* T, bf16* W, int np,
+                          float* d, void* X0, int x0_mode, bf16* T, bf16* W, int np,
                           int mp) {
   const int rows = T ? np : n, cols = T ? mp : m;
+  hipLaunchKernelGGL(w_norm_partials, dim3(ceil_div(m, DR_COLS), ceil_div(n, DR_ROWS), B),
+                     dim3(256), 0, st, A, n, m, w.U, w.V, w.kint, w.cw, w.wflag, w.wpart);
+  DMH_CHECK_LAUNCH("w_norm_partials");
   dim3 grid(ceil_div(cols, DR_COLS), ceil_div(rows, DR_ROWS), B);
   hipLaunchKernelGGL(deflate_restore, grid, dim3(256), 0, st, A, n, m, w.U, w.V, w.kint, w.cw,
-                     w.cr, d, X0, x0_mode, T, W, np, mp);
+                     w.cr, d, w.wflag, w.wpart, X0, x0_mode, T, W, np, mp);
   DMH_CHECK_LAUNCH("deflate_restore");
   return DMH_OK;
 }
@@ -1681,7 +1784,7 @@ int dmh_project(hipStream_t stream, const float* Q, const float* A, int batch, i
   GateParams gp{r, 1, 0.f, 0.f, 1.f};
   hipLaunchKernelGGL(eig_gate, dim3(batch), dim3(EG_THREADS), 0, stream, w.gram, gp, w.degen, w.s, RP,
                      w.Ub, w.UbS, w.k64, w.kint, w.cw, w.cr, (const double*)nullptr,
-                     (const double*)nullptr, 0, (float*)nullptr);
+                     (const double*)nullptr, 0, (float*)nullptr, (int*)nullptr);
   DMH_CHECK_LAUNCH("eig_gate");
   if ((rc = launch_uv(stream, w, batch, n, m))) return rc;
   return copy_usv(stream, w, batch, n, m, r, U, s, V);

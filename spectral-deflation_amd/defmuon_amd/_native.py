@@ -30,6 +30,9 @@ _SIGS = {
     "dmh_ns_chain_noalloc": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_ll,
                                      c_vp, c_int, c_int, ctypes.POINTER(ctypes.c_double),
                                      c_int]),
+    "dmh_horner_f32_workspace_size": (c_int, [c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
+    "dmh_horner_f32": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp,
+                               ctypes.POINTER(ctypes.c_double), c_int, c_vp, c_sz]),
     "dmh_rsvd_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
     "dmh_rmfro_workspace_size": (c_int, [c_int, c_int, c_int, c_int, ctypes.POINTER(c_sz)]),
     "dmh_orth": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_sz]),
@@ -148,6 +151,29 @@ def ns_chain(X, orient_tall, entry_mode, coeffs, out=None):
 
 def _ptr(t):
     return c_vp(t.data_ptr())
+
+
+def horner_f32(X, coeffs):
+    """The tall-convention chain in fp32 on a (batch, n, m) stack: per (a, b, c),
+    G = X^T X, B = bG + (cG)G, X <- aX + XB.  Returns a new fp32 tensor."""
+    _require_gpu(X, "horner_f32")
+    if X.ndim != 3:
+        raise NativeError(f"horner_f32 expects (batch, n, m), got {tuple(X.shape)}")
+    X = X.float().contiguous()
+    B, n, m = X.shape
+    out = torch.empty_like(X)
+    if B == 0:
+        return out
+    lib = load()
+    nbytes = c_sz()
+    _check(lib.dmh_horner_f32_workspace_size(B, n, m, ctypes.byref(nbytes)),
+           "dmh_horner_f32_workspace_size")
+    ws = _workspace(nbytes.value, X.device)
+    steps = len(coeffs)
+    flat = (ctypes.c_double * max(3 * steps, 1))(*[float(v) for t in coeffs for v in t])
+    _check(lib.dmh_horner_f32(_stream(X.device), _ptr(X), B, n, m, _ptr(out), flat, steps,
+                              _ptr(ws), nbytes.value), "dmh_horner_f32")
+    return out
 
 
 def _f32c(t, what):

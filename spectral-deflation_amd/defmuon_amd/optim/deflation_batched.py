@@ -141,11 +141,21 @@ def batched_rmfro_clip(A, generator=None, Omega=None, out_dtype=None, pad=DIVISO
 
 def _horner_iterate(X, hs):
     """X <- aX + bX^3 + cX^5 per (a, b, c) in hs, tall convention
-    (G = X^T X, X <- aX + X(bG + cG^2)), on a (B, n, m) bf16 batch in one grouped
-    launch per GEMM phase."""
+    (G = X^T X, X <- aX + X(bG + cG^2)), on a (B, n, m) or (n, m) batch in one
+    grouped launch per GEMM phase, in X's dtype (deflation_batched.py:196-204):
+    bf16 through the bf16 MFMA chain (the training path), fp32 through the fp32
+    chain (the reference's convergence study runs this function in fp32).  Other
+    dtypes raise NativeError."""
     squeeze = X.ndim == 2
     Xb = X[None] if squeeze else X
-    out = _native.ns_chain(Xb, True, 0, [tuple(h) for h in hs])
+    hs = [tuple(h) for h in hs]
+    if X.dtype == torch.bfloat16:
+        out = _native.ns_chain(Xb, True, 0, hs)
+    elif X.dtype == torch.float32:
+        out = _native.horner_f32(Xb, hs)
+    else:
+        raise _native.NativeError(f"_horner_iterate: {X.dtype} input is not supported "
+                                  "(bf16 or fp32)")
     return out[0] if squeeze else out
 
 

@@ -255,3 +255,30 @@ def test_rsvd_ragged_shapes_match_oracle(N, B, n, m, ns):
     assert torch.equal(k.cpu(), ko)
     np.testing.assert_allclose(d.cpu().numpy(), do.numpy(), rtol=1e-4)
     assert rel(X0.float().cpu(), Xo.float()) < 4e-3
+
+
+@pytest.mark.parametrize("bulk", [1e-3, 1e-4])
+def test_head_dominated_divisor(N, bulk):
+    """Rank-1 matrices with a bulk at `bulk` of sigma_1 (the head holds all but
+    ~m bulk^2 of the energy): d = ||A - U_k S_k V_k^T||_F + 1e-7 must match the
+    reference's explicit norm (the oracle) to 1e-4 and the entry must stay finite.
+    The algebraic ||A||^2 - sum lambda (2 - G) loses its digits here (its error grows
+    as ||A||^2 / ||W||^2), so the library recomputes d from W for such matrices."""
+    B, n, m = 4, 512, 512
+    g = torch.Generator().manual_seed(int(1 / bulk))
+    A = torch.empty(B, n, m)
+    for b in range(B):
+        u = torch.randn(n, 1, generator=g, dtype=torch.float64)
+        v = torch.randn(m, 1, generator=g, dtype=torch.float64)
+        noise = torch.randn(n, m, generator=g, dtype=torch.float64) / (n ** 0.5 + m ** 0.5)
+        A[b] = ((u / u.norm()) @ (v / v.norm()).mT + bulk * noise).float()
+    r, kw = O.sketch_dims(m)
+    Om = O.draw_omega(B, m, r, seed=5)
+    X0, k, d = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, O.GATE_RATIO, O.DEFLATE_THRESH,
+                            O.DIVISOR_PAD, out_dtype=torch.float32)
+    X0o, ko, do = O.rmfro_clip(A, Om)
+    assert k.cpu().tolist() == ko.tolist() == [1] * B
+    np.testing.assert_allclose(d.cpu().numpy(), do.numpy(), rtol=1e-4)
+    assert bool(torch.isfinite(X0).all())
+    # the deflated entry: 1/pad on the head, the bulk at unit Frobenius norm
+    assert rel(X0, X0o) < 1e-3

@@ -113,3 +113,24 @@ def test_config2_shape_deflated_iteration(N):
     want = O.horner_iterate(X0, O.ns_schedule(5))
     got = N.ns_chain(X0.to(DEV), True, 0, O.ns_schedule(5))
     assert_polar_parity(got[0], want[0], A, "config2 deflated ns")
+
+
+@pytest.mark.parametrize("shape,sched", [((2, 320, 96), "ns"), ((1, 768, 256), "pe")])
+def test_horner_fp32_keeps_dtype(N, shape, sched):
+    """_horner_iterate keeps X's dtype (deflation_batched.py:196-204): fp32 input runs
+    the fp32 chain and comes back fp32, within 1e-5 of the oracle's fp32 chain (the
+    reference's convergence study runs this function in fp32)."""
+    from defmuon_amd.optim import deflation_batched as DB
+    g = torch.Generator().manual_seed(sum(shape))
+    X = torch.randn(*shape, generator=g)
+    X = X / X.norm(dim=(-2, -1), keepdim=True)
+    hs = O.ns_schedule(5) if sched == "ns" else O.pe_schedule(5)
+    want = O.horner_iterate(X, hs)
+    got = DB._horner_iterate(X.to(DEV), hs)
+    assert got.dtype == torch.float32 and got.shape == X.shape
+    assert rel(got, want) <= 1e-5
+    got2 = DB._horner_iterate(X[0].to(DEV), hs)
+    assert got2.dtype == torch.float32 and got2.shape == X[0].shape
+    assert rel(got2, want[0]) <= 1e-5
+    with pytest.raises(N.NativeError):
+        DB._horner_iterate(X.to(DEV).half(), hs)
