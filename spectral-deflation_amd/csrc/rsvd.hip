@@ -1196,9 +1196,16 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
 constexpr int DR_ROWS = 64, DR_COLS = 128;
 constexpr int DR_KC = 16;   // head columns staged per chunk
 
-// restore tiles per matrix (also the count of w_norm_partials' partials)
+// restore tiles per matrix
 __host__ __device__ inline int wn_tiles(int n, int m) {
   return ((m + DR_COLS - 1) / DR_COLS) * ((n + DR_ROWS - 1) / DR_ROWS);
+}
+
+// w_norm_partials' workgroups (and partial sums) per matrix
+constexpr int WN_PARTS = 32;
+__host__ __device__ inline int wn_parts(int n, int m) {
+  const int t = wn_tiles(n, m);
+  return t < WN_PARTS ? t : WN_PARTS;
 }
 
 // LDS of one restore tile: the head chunk (U rows of the tile, V rows of the tile
@@ -1228,7 +1235,7 @@ __global__ __launch_bounds__(256) void deflate_restore(
   if (wflag && wflag[b]) {
     // d from W itself: every workgroup sums the same partials in the same order
     // (so all agree on d bit for bit); the first stores it as the API's d
-    const int nt = wn_tiles(n, m);
+    const int nt = wn_parts(n, m);
     __shared__ double wsum[256];
     double acc = 0.0;
     for (int t = tid; t < nt; t += 256) acc += wpart[(long long)b * nt + t];
@@ -1334,8 +1341,10 @@ __global__ __launch_bounds__(256) void deflate_restore(
 
 // Explicit ||W||_F^2 for the matrices eig_gate flagged (head energy above 99% of
 // ||A||^2): W = A - U diag(cw) V^T over the restore's 64 x 128 tiles, per-thread
-// squares summed in fp64, one partial per tile (wpart[b][tile]); other matrices'
-// workgroups return at once.  deflate_restore turns the partials into d.
+// squares summed in fp64.  wn_parts() workgroups per matrix stride over its tiles,
+// one partial each (wpart[b][part]); other matrices' workgroups return at once, so
+// the common case costs B * WN_PARTS empty workgroups.  deflate_restore turns the
+// partials into d.
 __global__ __launch_bounds__(256) void w_norm_partials(
     const float* __restrict__ A, int n, int m, const float* __restrict__ U,
     const float* __restrict__ V, const int* __restrict__ kvec, const float* __restrict__ cw,
@@ -1345,60 +1354,63 @@ __global__ __launch_bounds__(256) void w_norm_partials(
   __shared__ __attribute__((aligned(16))) RestoreLds sm;
   __shared__ float coef[RP];
   __shared__ double red[256];
-  const int i0 = blockIdx.y * DR_ROWS, j0 = blockIdx.x * DR_COLS;
   const int tid = threadIdx.x;
   const int k = kvec[b];
   const float* Ab = A + (long long)b * n * m;
   const int c4 = (tid & 31) * 4, rw = tid >> 5;
-  float x[8][4];
-#pragma unroll
-  for (int a = 0; a < 8; ++a)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
-      x[a][c] = (gi < n && gj < m) ? Ab[(long long)gi * m + gj] : 0.f;
-    }
+  const int tiles_x = (m + DR_COLS - 1) / DR_COLS, ntiles = wn_tiles(n, m);
   if (tid < RP) coef[tid] = cw[b * RP + tid];
-  for (int t0 = 0; t0 < k; t0 += DR_KC) {
-    const int kc = min(DR_KC, k - t0);
-    __syncthreads();
-    for (int e = tid; e < DR_ROWS * DR_KC; e += 256) {
-      const int rr = e / DR_KC, t = e % DR_KC, gi = i0 + rr;
-      sm.head.Us[rr][t] = (t < kc && gi < n) ? U[((long long)b * n + gi) * RP + t0 + t] : 0.f;
-    }
-    for (int e = tid; e < DR_COLS * DR_KC; e += 256) {
-      const int cc = e / DR_KC, t = e % DR_KC, gj = j0 + cc;
-      sm.head.Vt[t][cc] = (t < kc && gj < m) ? V[((long long)b * m + gj) * RP + t0 + t] : 0.f;
-    }
-    __syncthreads();
-    for (int t = 0; t < kc; ++t) {
-      const float4 v = *(const float4*)&sm.head.Vt[t][c4];
-      const float ct = coef[t0 + t];
+  double sq = 0.0;
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int i0 = (tile / tiles_x) * DR_ROWS, j0 = (tile % tiles_x) * DR_COLS;
+    float x[8][4];
 #pragma unroll
-      for (int a = 0; a < 8; ++a) {
-        const float u = sm.head.Us[rw + 8 * a][t] * ct;
-        x[a][0] = fmaf(-u, v.x, x[a][0]);
-        x[a][1] = fmaf(-u, v.y, x[a][1]);
-        x[a][2] = fmaf(-u, v.z, x[a][2]);
-        x[a][3] = fmaf(-u, v.w, x[a][3]);
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
+        x[a][c] = (gi < n && gj < m) ? Ab[(long long)gi * m + gj] : 0.f;
+      }
+    for (int t0 = 0; t0 < k; t0 += DR_KC) {
+      const int kc = min(DR_KC, k - t0);
+      __syncthreads();   // coef written; the previous chunk's readers done
+      for (int e = tid; e < DR_ROWS * DR_KC; e += 256) {
+        const int rr = e / DR_KC, t = e % DR_KC, gi = i0 + rr;
+        sm.head.Us[rr][t] = (t < kc && gi < n) ? U[((long long)b * n + gi) * RP + t0 + t] : 0.f;
+      }
+      for (int e = tid; e < DR_COLS * DR_KC; e += 256) {
+        const int cc = e / DR_KC, t = e % DR_KC, gj = j0 + cc;
+        sm.head.Vt[t][cc] = (t < kc && gj < m) ? V[((long long)b * m + gj) * RP + t0 + t] : 0.f;
+      }
+      __syncthreads();
+      for (int t = 0; t < kc; ++t) {
+        const float4 v = *(const float4*)&sm.head.Vt[t][c4];
+        const float ct = coef[t0 + t];
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+          const float u = sm.head.Us[rw + 8 * a][t] * ct;
+          x[a][0] = fmaf(-u, v.x, x[a][0]);
+          x[a][1] = fmaf(-u, v.y, x[a][1]);
+          x[a][2] = fmaf(-u, v.z, x[a][2]);
+          x[a][3] = fmaf(-u, v.w, x[a][3]);
+        }
       }
     }
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
+        if (gi < n && gj < m) sq += (double)x[a][c] * (double)x[a][c];
+      }
   }
-  double sq = 0.0;
-#pragma unroll
-  for (int a = 0; a < 8; ++a)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
-      if (gi < n && gj < m) sq += (double)x[a][c] * (double)x[a][c];
-    }
   red[tid] = sq;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
     if (tid < w) red[tid] += red[tid + w];
     __syncthreads();
   }
-  if (tid == 0) wpart[(long long)b * wn_tiles(n, m) + blockIdx.y * gridDim.x + blockIdx.x] = red[0];
+  if (tid == 0) wpart[(long long)b * wn_parts(n, m) + blockIdx.x] = red[0];
 }
 
 // strided copy of the first r of RP columns: dst (B, rows, r) contiguous
@@ -1509,7 +1521,7 @@ static RsvdWs rsvd_layout(void* base, int B, int n, int m) {
   w.kint = (int*)take((size_t)B * sizeof(int));
   w.degen = (int*)take((size_t)B * sizeof(int));
   w.wflag = (int*)take((size_t)B * sizeof(int));
-  w.wpart = (double*)take((size_t)B * wn_tiles(n, m) * sizeof(double));
+  w.wpart = (double*)take((size_t)B * WN_PARTS * sizeof(double));
   if (sk_fast(n, m)) {
     int S, rps;
     sk_splits(B, n, m, &S, &rps);
@@ -1679,7 +1691,7 @@ static int launch_restore(hipStream_t st, const float* A, int B, int n, int m, c
                           float* d, void* X0, int x0_mode, bf16* T, bf16* W, int np,
                           int mp) {
   const int rows = T ? np : n, cols = T ? mp : m;
-  hipLaunchKernelGGL(w_norm_partials, dim3(ceil_div(m, DR_COLS), ceil_div(n, DR_ROWS), B),
+  hipLaunchKernelGGL(w_norm_partials, dim3(wn_parts(n, m), 1, B),
                      dim3(256), 0, st, A, n, m, w.U, w.V, w.kint, w.cw, w.wflag, w.wpart);
   DMH_CHECK_LAUNCH("w_norm_partials");
   dim3 grid(ceil_div(cols, DR_COLS), ceil_div(rows, DR_ROWS), B);
