@@ -35,6 +35,8 @@ PEAK_HBM_GBS = 8000.0
 # tall-shape groups (batch, n, m) of one polar step, after the W_QKV split and the
 # wide -> tall transpose (muon.py:275-285); GPT-2 Linear weights are (out, in)
 WORKLOADS = {
+    # config 2: one spiked 768 x 3072 momentum, transposed to tall by Muon
+    "config2": [(1, 3072, 768)],
     "gpt2-small": [(48, 768, 768), (24, 3072, 768)],
     "gpt2-medium": [(96, 1024, 1024), (48, 4096, 1024)],
     "gpt2-large": [(144, 1280, 1280), (72, 5120, 1280)],
@@ -45,6 +47,8 @@ WORKLOADS = {
 # (out, in) layout, grouped as the grouped plain step launches them:
 # (count, rows, cols, tall) -- tall: the factorizer runs on the transpose
 PLAIN_GROUPS = {
+    # config 1: ns5 on one 768 x 3072 matrix with N(0, 1) entries (seed 0)
+    "config1": [(1, 768, 3072, False)],
     "gpt2-small": [(48, 768, 768, False), (12, 3072, 768, True), (12, 768, 3072, False)],
     "gpt2-medium": [(96, 1024, 1024, False), (24, 4096, 1024, True), (24, 1024, 4096, False)],
     "gpt2-large": [(144, 1280, 1280, False), (36, 5120, 1280, True), (36, 1280, 5120, False)],
@@ -55,20 +59,41 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+CHAIN_SOURCES = ("common.h", "ns_chain.h", "ns_chain.hip")
+
+
+def chain_sources_sha256():
+    """sha256 over the NS chain's sources (csrc/common.h, ns_chain.h, ns_chain.hip, in
+    that order): stamps counter measurements of the chain's kernels, so a measurement
+    is used only with the kernels it was taken on."""
+    import hashlib
+    d = os.path.join(ROOT, "spectral-deflation_amd", "csrc")
+    h = hashlib.sha256()
+    for name in CHAIN_SOURCES:
+        h.update(name.encode())
+        with open(os.path.join(d, name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def ns_flops(groups, steps=5):
     """Canonical dense NS FLOPs: 4 m^2 n + 2 m^3 per matrix and iteration."""
     return sum(B * steps * (4 * m * m * n + 2 * m ** 3) for B, n, m in groups)
 
 
 def make_inputs(groups, device, seed=1234, kind="spiked"):
-    """Synthetic momenta per group.  "gaussian": i.i.d. N(0, 1/n) entries (no QR, so
-    nothing from the solver library runs; the gate declines every matrix), for
-    hardware-counter runs whose NS-chain traffic does not depend on the values."""
+    """Synthetic momenta per group.  "spiked": generated on the GPU; "spiked-cpu":
+    the same construction on the host (its QRs run in the CPU solver), then copied
+    to the GPU -- for hardware-counter runs, which should not run the GPU solver
+    library; "gaussian": i.i.d. N(0, 1/n) entries (the gate declines every matrix)."""
     import torch
     from defmuon_amd import synthetic as S
     out = []
     for gi, (B, n, m) in enumerate(groups):
-        if kind == "gaussian":
+        if kind == "spiked-cpu":
+            out.append(S.spiked_batch(B, n, m, seed=seed + gi, n_spikes=8, hi=50.0, lo=10.0,
+                                      device="cpu").to(device))
+        elif kind == "gaussian":
             g = torch.Generator(device=device)
             g.manual_seed(seed + gi)
             out.append(torch.randn(B, n, m, device=device, generator=g) / math.sqrt(n))
@@ -105,10 +130,16 @@ def polar_step(fac, stacks, bd_step, ns_steps, events=None):
     return outs
 
 
-def make_plain_inputs(pgroups, device, seed=4321):
-    """Spiked-spectrum momenta per plain group, in the parameters' own layout."""
+def make_plain_inputs(pgroups, device, seed=4321, gaussian=False):
+    """Spiked-spectrum momenta per plain group, in the parameters' own layout
+    (gaussian: N(0, 1) entries from torch.Generator().manual_seed(0), config 1)."""
+    import torch
     from defmuon_amd import synthetic as S
     out = []
+    if gaussian:
+        g = torch.Generator().manual_seed(0)
+        return [torch.randn(B, rows, cols, generator=g).to(device)
+                for B, rows, cols, _ in pgroups]
     for gi, (B, rows, cols, tall) in enumerate(pgroups):
         n, m = max(rows, cols), min(rows, cols)
         X = S.spiked_batch(B, n, m, seed=seed + gi, n_spikes=8, hi=50.0, lo=10.0, device=device)
@@ -315,6 +346,233 @@ def cpu_baseline(groups, arm, min_s=12.0, max_reps=20):
             "cpu": _cpu_model()}
 
 
+# Algorithmic bytes per element of a group's (n x m) matrices for the memory-bound
+# kernels, per launch: fp32 reads 4 B, bf16 reads/writes 2 B, fp32 writes 4 B.
+KERNEL_BYTES = {
+    "sk_rows": 4,            # A read (A Omega, A Z)
+    "sk_cols": 4,            # A read (A^T Q)
+    "deflate_restore": 6,    # A read fp32, the chain's packed bf16 T written
+    "entry_norm_partials": 4,  # X read fp32
+    "entry_pack": 6,         # X read fp32, packed bf16 T written
+    "momentum_stack": 16,    # grad and buffer read, buffer and fp32 stack written
+    "apply_update": 10,      # parameter read and written fp32, bf16 update read
+}
+
+
+def kernels_report(args, dev):
+    """--mode kernels: the memory-bound kernels of the path, each group's launches
+    one after the other on one stream (nothing overlapping), `args.steps` rounds,
+    for rocprofv3 --kernel-trace --stats; then --summarize-trace turns the stats
+    into GB/s.  Per round and shape group: the deflated front-end
+    (dmh_deflated_polar_front: sk_rows x2, sk_cols x2, deflate_restore), the plain
+    arms' fp32 entry (dmh_ns_chain with zero steps: entry_norm_partials, entry_pack,
+    copy_out) and the optimizer glue (dmh_momentum_stack, dmh_apply_update)."""
+    import torch
+    from defmuon_amd import _native
+    from defmuon_amd.optim import deflation_batched as DB
+    groups = WORKLOADS[args.workload]
+    stacks = make_inputs(groups, dev, kind=args.inputs)
+    glue = []
+    for (B, n, m), A in zip(groups, stacks):
+        g = torch.randn(B, n, m, device=dev) * 1e-2
+        buf = torch.zeros(B, n, m, device=dev)
+        par = torch.randn(B, n, m, device=dev) * 2e-2
+        stack = torch.empty(B, n, m, device=dev)
+        u = torch.empty(B, n, m, dtype=torch.bfloat16, device=dev)
+        ps = []
+        for b in range(B):
+            d = _native.GlueParam()
+            d.grad, d.momentum, d.param = g[b].data_ptr(), buf[b].data_ptr(), par[b].data_ptr()
+            d.rows, d.cols, d.blocks, d.transpose = n, m, 1, 0
+            d.offset, d.alpha, d.decay = b * n * m, -1e-3, 1.0
+            ps.append(d)
+        glue.append((ps, stack, u, (g, buf, par)))
+    torch.cuda.synchronize()
+    for rnd in range(args.warmup + args.steps):
+        for gi, ((B, n, m), A) in enumerate(zip(groups, stacks)):
+            r, kw = DB.sketch_dims(m)
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(rnd * 1009 + gi)
+            Om = torch.randn(B, m, r, device=dev, generator=gen)
+            _native.deflated_polar_front(A, Om, kw, DB.GATE_RATIO, DB.DEFLATE_THRESH,
+                                         DB.DIVISOR_PAD, DB.RSVD_NITER, DB.CHOLQR_PASSES)
+            _native.ns_chain(A, True, 1, [])
+            ps, stack, u, _ = glue[gi]
+            _native.momentum_stack(ps, 0.95, True, stack)
+            _native.apply_update(ps, u)
+        torch.cuda.synchronize()
+    log(f"bench kernels: {args.warmup} + {args.steps} rounds over {groups}")
+    return {"mode": "kernels", "workload": args.workload, "groups": groups,
+            "rounds": args.warmup + args.steps}
+
+
+def summarize_trace(path, workload, rounds):
+    """GB/s of the memory-bound kernels from a rocprofv3 --stats kernel_stats.csv of
+    `bench.py --mode kernels` (algorithmic bytes KERNEL_BYTES per element, summed
+    over the groups of every round, over the kernels' total duration)."""
+    import csv
+    groups = WORKLOADS[workload]
+    elems = sum(B * n * m for B, n, m in groups)
+    per_round_launches = {"sk_rows": 2, "sk_cols": 2}
+    rows = list(csv.DictReader(open(path)))
+    print("| kernel | launches | avg us | algorithmic GB per launch | achieved GB/s | "
+          "fraction of 8 TB/s |")
+    print("|---|---|---|---|---|---|")
+    for name, bpe in KERNEL_BYTES.items():
+        hit = [r for r in rows if name in r["Name"]]
+        if not hit:
+            continue
+        calls = sum(int(r["Calls"]) for r in hit)
+        tot_ns = sum(float(r["TotalDurationNs"]) for r in hit)
+        nbytes = rounds * per_round_launches.get(name, 1) * bpe * elems
+        gbs = nbytes / tot_ns
+        print(f"| `{name}` | {calls} | {tot_ns / calls / 1e3:.1f} | {nbytes / calls / 1e9:.3f} | "
+              f"{gbs:.0f} | {gbs / PEAK_HBM_GBS:.2f} |")
+
+
+GEMM_LABELS = {
+    "dmh::gemm_nt_bf16<0, 0>": "K3 T' = T B'",
+    "dmh::gemm_nt_bf16<0, 1>": "K1 A = T^T T, K-major",
+    "dmh::gemm_nt_bf16<1, 0>": "K2 B' = bA + cA^2 + aI",
+}
+
+
+def _dmh_kernel(name):
+    """Short name of one of the library's kernels (None for any other kernel)."""
+    import re
+    name = name.replace("void ", "")
+    m = re.match(r"(dmh::[A-Za-z_0-9]+(<[^>]*>)?)", name)
+    if m:
+        return m.group(1)
+    m = re.match(r"_ZN3dmh(\d+)", name)
+    if m:
+        n = int(m.group(1))
+        return "dmh::" + name[len("_ZN3dmh") + len(m.group(1)):][:n]
+    return None
+
+
+def summarize_step_trace(path, steps, warmup):
+    """Per-polar-step table of the library's kernels from a rocprofv3 --kernel-trace
+    kernel_trace.csv (plain or .gz) of `bench.py --steps S --warmup W`: the chain's
+    GEMMs over the S steps of the sequential pass (launch stream, Stream_Id 0), every
+    other kernel over all W + 2S steps."""
+    import collections
+    import csv
+    import gzip
+    opener = gzip.open if path.endswith(".gz") else open
+    with opener(path, "rt") as f:
+        rows = list(csv.DictReader(f))
+    all_steps = warmup + 2 * steps
+    agg = collections.OrderedDict()
+    for r in rows:
+        k = _dmh_kernel(r["Kernel_Name"])
+        if not k:
+            continue
+        gemm = "gemm_nt" in k
+        if gemm and r["Stream_Id"] != "0":
+            continue
+        a = agg.setdefault(k, [0, 0, gemm])
+        a[0] += 1
+        a[1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    per_step = {k: t / (steps if g else all_steps) for k, (c, t, g) in agg.items()}
+    print("| kernel | calls | total ms | avg us | ms per polar step |")
+    print("|---|---|---|---|---|")
+    ns_t = ns_c = 0
+    for k in sorted(agg, key=lambda k: -per_step[k]):
+        c, t, gemm = agg[k]
+        label = f"`{k}`" + (f" ({GEMM_LABELS[k]})" if k in GEMM_LABELS else "")
+        print(f"| {label} | {c} | {t / 1e6:.2f} | {t / 1e3 / c:.1f} | {per_step[k] / 1e6:.2f} |")
+        if gemm:
+            ns_t += t
+            ns_c += c
+    print(f"| **NS chain (gemm_nt_bf16)** | {ns_c} | {ns_t / 1e6:.2f} | | "
+          f"**{ns_t / 1e6 / steps:.2f}** |")
+    print(f"| **all library kernels** | | | | {sum(per_step.values()) / 1e6:.2f} |")
+
+
+def summarize_pmc(paths, steps_in_trace, copy_mib=0, traffic_json=None):
+    """Per-kernel sums of rocprofv3 --pmc counter_collection.csv files taken over
+    `bench.py --steps S --warmup W` (steps_in_trace = W + S + the S steps of the
+    NS-chain pass), per polar step.  FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are
+    scaled by what they read for torch's copy kernel over --copy-calibration MiB
+    (3 copies: FETCH should see the bytes read, WRITE the bytes written); with
+    traffic_json the NS chain's traffic per step is written there, stamped with
+    the NS chain sources' sha256.  MFMA utilisation = SQ_VALU_MFMA_BUSY_CYCLES /
+    (4 SIMDs x SQ_BUSY_CU_CYCLES) per kernel."""
+    import collections
+    import csv
+    sums = collections.OrderedDict()
+    disp = collections.defaultdict(set)     # per kernel: (file, dispatch) pairs
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"]
+            short = ("copy (calibration)" if "copy" in name.lower() and "dmh" not in name else
+                     name.split("(")[0].replace("void ", "").strip())
+            key = short
+            sums.setdefault(key, collections.defaultdict(float))
+            sums[key][r["Counter_Name"]] += float(r["Counter_Value"])
+            disp[key].add((path, r["Dispatch_Id"]))
+    scale = {}
+    if copy_mib and "copy (calibration)" in sums:
+        cal = sums["copy (calibration)"]
+        nbytes = 3 * copy_mib * 2 ** 20
+        if cal.get("FETCH_SIZE"):
+            scale["FETCH_SIZE"] = nbytes / (cal["FETCH_SIZE"] * 1024)
+        if cal.get("WRITE_SIZE"):
+            scale["WRITE_SIZE"] = nbytes / (cal["WRITE_SIZE"] * 1024)
+    counters = sorted({c for v in sums.values() for c in v})
+    print("| kernel | dispatches per step | " + " | ".join(
+        c + (" (GB/step)" if c in ("FETCH_SIZE", "WRITE_SIZE") else " (/step)") for c in counters)
+        + (" | MFMA util |" if "SQ_VALU_MFMA_BUSY_CYCLES" in counters else " |"))
+    print("|---|---|" + "---|" * len(counters) + ("---|" if "SQ_VALU_MFMA_BUSY_CYCLES" in counters else ""))
+    chain = collections.defaultdict(float)
+    for key, v in sums.items():
+        if key == "copy (calibration)":
+            continue
+        cells = []
+        for c in counters:
+            x = v.get(c, 0.0) / steps_in_trace
+            if c in ("FETCH_SIZE", "WRITE_SIZE"):
+                x = x * 1024 * scale.get(c, 1.0) / 1e9
+                if "gemm" in key:
+                    chain[c] += x
+                cells.append(f"{x:.2f}")
+            else:
+                cells.append(f"{x:.4g}")
+        util = ""
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in counters:
+            busy = v.get("SQ_BUSY_CU_CYCLES", 0.0)
+            util = f" {v.get('SQ_VALU_MFMA_BUSY_CYCLES', 0.0) / (4 * busy):.3f} |" if busy else " - |"
+        per_file = max(sum(1 for p, _ in disp[key] if p == path) for path in paths)
+        print(f"| `{key}` | {per_file / steps_in_trace:.1f} | " + " | ".join(cells) + " |" + util)
+    if scale:
+        print()
+        print("scale factors from the copy calibration: " +
+              ", ".join(f"{c} x{v:.3f}" for c, v in scale.items()))
+    if chain:
+        print("NS chain (gemm) per step: " + ", ".join(f"{c} {v:.2f} GB" for c, v in chain.items()))
+    if traffic_json and chain:
+        rec = {}
+        if os.path.exists(traffic_json):
+            with open(traffic_json) as f:
+                rec = json.load(f)
+        if rec.get("ns_chain_sources_sha256") != chain_sources_sha256():
+            rec = {}
+        if "FETCH_SIZE" in chain:
+            rec["ns_chain_read_bytes_per_step"] = chain["FETCH_SIZE"] * 1e9
+            rec["fetch_scale"] = scale.get("FETCH_SIZE")
+        if "WRITE_SIZE" in chain:
+            rec["ns_chain_write_bytes_per_step"] = chain["WRITE_SIZE"] * 1e9
+            rec["write_scale"] = scale.get("WRITE_SIZE")
+        if "ns_chain_read_bytes_per_step" in rec and "ns_chain_write_bytes_per_step" in rec:
+            rec["ns_chain_hbm_bytes_per_step"] = (rec["ns_chain_read_bytes_per_step"] +
+                                                  rec["ns_chain_write_bytes_per_step"])
+        rec["ns_chain_sources_sha256"] = chain_sources_sha256()
+        rec["source"] = "profiles/polar_step_gpt2_large_hbm_traffic.md"
+        with open(traffic_json, "w") as f:
+            json.dump(rec, f, indent=1)
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -330,21 +588,52 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="gpt2-large", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="gpt2-large",
+                    choices=sorted(set(WORKLOADS) | set(PLAIN_GROUPS)),
+                    help="config1: ns5 on one 768x3072 matrix; config2: one deflated "
+                         "3072x768 matrix; gpt2-small / -medium / -large: every Muon matrix "
+                         "of the model (configs 3, 4, 5)")
     ap.add_argument("--arm", default="deflated_ns_cut",
                     choices=["deflated_ns_cut", "deflated_pe_cut", "ns5", "polarexpress"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--inputs", default="spiked", choices=["spiked", "gaussian"],
-                    help="synthetic momenta: spiked spectra (default) or i.i.d. Gaussian "
-                         "(for counter runs; no solver call)")
-    ap.add_argument("--mode", default="polar", choices=["polar", "train"],
+    ap.add_argument("--inputs", default="spiked", choices=["spiked", "spiked-cpu", "gaussian"],
+                    help="synthetic momenta: spiked spectra generated on the GPU (default), "
+                         "the same generated on the host (counter runs: no GPU solver "
+                         "call), or i.i.d. Gaussian")
+    ap.add_argument("--mode", default="polar", choices=["polar", "train", "kernels"],
                     help="polar: the polar-step bench (default); train: the GPT-2-large "
-                         "training step of config 5, with the polar-factor share")
+                         "training step of config 5, with the polar-factor share; kernels: "
+                         "the memory-bound kernels one after the other, for a rocprofv3 "
+                         "kernel trace (see --summarize-trace)")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="COUNTER_CSV",
+                    help="print per-kernel counter sums per polar step of rocprofv3 --pmc "
+                         "counter_collection.csv files taken over this bench with the same "
+                         "--steps/--warmup (and --copy-calibration)")
+    ap.add_argument("--traffic-json", metavar="PATH",
+                    help="with --summarize-pmc: write the NS chain's FETCH/WRITE bytes per "
+                         "step there, stamped with the NS chain sources' sha256")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_STATS_CSV",
+                    help="print the GB/s table of a rocprofv3 --stats kernel_stats.csv taken "
+                         "over --mode kernels with the same --workload/--steps/--warmup")
+    ap.add_argument("--summarize-step-trace", metavar="KERNEL_TRACE_CSV",
+                    help="print the per-polar-step table of the library's kernels from a "
+                         "rocprofv3 --kernel-trace kernel_trace.csv (or .csv.gz) taken over "
+                         "this bench with the same --steps/--warmup")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="before the steps, copy a MIB-MiB fp32 buffer three times with "
                          "torch's copy kernel: a known-size reference for HBM byte "
                          "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc, args.warmup + 2 * args.steps, args.copy_calibration,
+                      args.traffic_json)
+        return
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.workload, args.warmup + args.steps)
+        return
+    if args.summarize_step_trace:
+        summarize_step_trace(args.summarize_step_trace, args.steps, args.warmup)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the polar path "
               "shards by matrix across GPUs, which this build does not run.", file=sys.stderr)
@@ -363,8 +652,14 @@ def main():
     if args.mode == "train":
         print(json.dumps(train_step_report(args, dev)), flush=True)
         return
-    groups = WORKLOADS[args.workload]
+    if args.mode == "kernels":
+        print(json.dumps(kernels_report(args, dev)), flush=True)
+        return
     plain = args.arm in ("ns5", "polarexpress")
+    if (plain and args.workload not in PLAIN_GROUPS) or (not plain and args.workload not in WORKLOADS):
+        print(f"bench.py: workload {args.workload} has no {args.arm} configuration", file=sys.stderr)
+        sys.exit(2)
+    groups = WORKLOADS.get(args.workload)
     fac = None if plain else C.ARMS[args.arm]()
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration * 2 ** 18, dtype=torch.float32, device=dev)
@@ -377,7 +672,7 @@ def main():
     if plain:
         pgroups = PLAIN_GROUPS[args.workload]
         log(f"bench: generating inputs for {args.workload} ({args.arm}): {pgroups}")
-        stacks = make_plain_inputs(pgroups, dev)
+        stacks = make_plain_inputs(pgroups, dev, gaussian=args.workload == "config1")
 
         def step(i, events=None):
             return plain_step(args.arm, stacks, pgroups, 5, events)
@@ -442,12 +737,18 @@ def main():
         cpu = cpu_baseline(groups, args.arm)
 
     nmat = sum(B for B, _, _ in groups)
-    # HBM traffic of the NS chain from the committed counter runs (same workload and arm)
+    # HBM traffic of the NS chain from the committed counter runs, used only when they
+    # were measured on this build (same workload and arm, same NS chain sources)
     traffic = {}
     tpath = os.path.join(ROOT, "profiles", "ns_chain_traffic.json")
     if args.workload == "gpt2-large" and args.arm == "deflated_ns_cut" and os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f)
+            rec = json.load(f)
+        if rec.get("ns_chain_sources_sha256") == chain_sources_sha256():
+            traffic = rec
+        else:
+            log("bench: profiles/ns_chain_traffic.json was measured on other NS chain sources; "
+                "roofline.traffic is null")
     out = {
         "metric": "polar steps/sec (GPT-2-large all matrices, 1 GPU) + % bf16 MFMA peak",
         "value": 1e3 / ms_per_step,
@@ -460,10 +761,13 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 (NS chain) / fp32+fp64 (rSVD front-end)",
-        "data": "synthetic: spiked-spectrum fp32 momenta (8 spikes 50x..10x over a "
-                "Marchenko-Pastur bulk, Haar singular vectors), resident in HBM",
+        "data": ("synthetic: one 768x3072 fp32 matrix with N(0, 1) entries (seed 0), "
+                 "resident in HBM" if args.workload == "config1" else
+                 "synthetic: spiked-spectrum fp32 momenta (8 spikes 50x..10x over a "
+                 "Marchenko-Pastur bulk, Haar singular vectors), resident in HBM"),
         "config": {"workload": f"{args.workload} {args.arm} polar step: "
-                               + " + ".join(f"{B}x({n},{m})" for B, n, m in groups),
+                               + " + ".join(f"{B}x({n},{m})" for B, n, m in groups)
+                               + " (tall convention: wide matrices run as their transpose)",
                    "matrices": nmat, "ns_steps": 5, "arm": args.arm},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,

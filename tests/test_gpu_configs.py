@@ -11,7 +11,7 @@ Config 5: GPT-2 large, deflated_ns_cut over 144 x (1280, 1280) and 72 x (5120, 1
 
 Every gate decision is checked exactly; the polar factors are checked against
 the oracle (same sketch, drawn with the reference's seed formula, muon.py:290-291)
-on a sample of matrices per group, with the tolerances of tests/parity.py.
+on 8 matrices spread over each group, with the tolerances of tests/parity.py.
 """
 
 import pytest
@@ -53,6 +53,13 @@ def _deflated_group(C, arm, A, gi, bd_step=1):
     return U, k, Om
 
 
+def _spread(B, count=8):
+    """`count` matrix indices spread over a batch of B (first and last included)."""
+    if B <= count:
+        return list(range(B))
+    return sorted({round(i * (B - 1) / (count - 1)) for i in range(count)})
+
+
 def _check_deflated_sample(arm, A, Om, U, idx):
     pad = O.DIVISOR_PAD if arm == "deflated_ns_cut" else O.PE_PAD
     hs = O.ns_schedule(5) if arm == "deflated_ns_cut" else O.pe_schedule(5)
@@ -71,7 +78,7 @@ def test_config3_gpt2_small_deflated(mods, arm):
         U, k, Om = _deflated_group(C, arm, A, gi)
         assert k.tolist() == [8] * B, k.tolist()
         assert torch.isfinite(U.float()).all()
-        _check_deflated_sample(arm, A, Om, U, [0, B - 1])
+        _check_deflated_sample(arm, A, Om, U, _spread(B))
 
 
 @pytest.mark.parametrize("arm", ["ns5", "polarexpress"])
@@ -110,12 +117,13 @@ def test_config4_gpt2_medium_pe(mods):
         assert want.count(12) == B - len(unspiked)
         assert k.tolist() == want, k.tolist()
         assert torch.isfinite(U.float()).all()
-        _check_deflated_sample("deflated_pe_cut", A, Om, U, [0, 1])
+        _check_deflated_sample("deflated_pe_cut", A, Om, U, _spread(B))
 
 
 def test_config5_gpt2_large_deflated(mods):
-    """The bench workload itself: every gate fires with k = 8, and the first and last
-    matrix of each group match the oracle on their own sketches."""
+    """The bench workload itself: every gate fires with k = 8, and 8 matrices spread
+    over each group (the first and last included) match the oracle on their own
+    sketches."""
     S, C, _, _ = mods
     for gi, (B, n, m) in enumerate(LARGE):
         A = S.spiked_batch(B, n, m, seed=500 + gi, n_spikes=8, hi=50.0, lo=10.0, device=DEV)
@@ -123,6 +131,61 @@ def test_config5_gpt2_large_deflated(mods):
         assert S.expected_k(8, 50.0, 10.0) == 8
         assert k.tolist() == [8] * B, k.tolist()
         assert torch.isfinite(U.float()).all()
-        _check_deflated_sample("deflated_ns_cut", A, Om, U, [0, B - 1])
+        _check_deflated_sample("deflated_ns_cut", A, Om, U, _spread(B))
         del A, U, Om
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("arm", ["ns5", "polarexpress"])
+def test_config3_grouped_plain_matches_oracle(mods, arm):
+    """The grouped plain-arm launch (grouped_plain.install(), one launch per (shape,
+    dtype, orientation) group) over GPT-2 small's full Muon parameter set -- 12
+    layers x {attn.c_attn as its (3, 768, 768) split, attn.c_proj, mlp.c_fc,
+    mlp.c_proj}, 72 matrices -- against the oracle's ns5 / PolarExpress on every
+    matrix (muon.py:361-386: the factorizer of each parameter's Nesterov momentum)."""
+    S, _, M, PE = mods
+    from defmuon_amd import _native
+    from defmuon_amd.optim import grouped_plain
+    d = 768
+    params, grads = {}, {}
+    for layer in range(12):
+        for name, shape in (("attn.c_attn", (3 * d, d)), ("attn.c_proj", (d, d)),
+                            ("mlp.c_fc", (4 * d, d)), ("mlp.c_proj", (d, 4 * d))):
+            key = f"h.{layer}.{name}.weight"
+            params[key] = torch.nn.Parameter(torch.zeros(shape, device=DEV))
+            seed = 3000 + 10 * layer + len(grads)
+            if name == "attn.c_attn":
+                g = torch.cat([S.spiked_matrix(d, d, seed=seed + j) for j in range(3)])
+            else:
+                g = S.spiked_matrix(*shape, seed=seed)
+            grads[key] = g.to(DEV)
+    launches = []
+    real = _native.ns_chain
+
+    def spy(X, tall, mode, sched, out=None):
+        res = real(X, tall, mode, sched, out)
+        launches.append((X.detach().clone(), tall, res.detach().clone()))
+        return res
+
+    grouped_plain.install()
+    try:
+        opt = M.Muon(list(params.items()), lr=0.01, weight_decay=0.0, momentum=0.95,
+                     nesterov=True, ns_steps=5, polar_method=arm)   # (its warm-up unspied)
+        _native.ns_chain = spy
+        for k, p in params.items():
+            p.grad = grads[k]
+        opt.step()
+        torch.cuda.synchronize()
+    finally:
+        _native.ns_chain = real
+        grouped_plain.uninstall()
+    # one launch per (shape, orientation) group: (768, 768) x 48, c_fc x 12, c_proj x 12
+    assert sorted(X.shape[0] for X, _, _ in launches) == [12, 12, 48]
+    ofn = O.ns5 if arm == "ns5" else O.polar_express
+    checked = 0
+    for X, tall, U in launches:
+        for i in range(X.shape[0]):
+            G = X[i].cpu()
+            assert_polar_parity(U[i].cpu(), ofn(G, 5), G, tag=f"grouped {arm} {tuple(G.shape)} #{i}")
+            checked += 1
+    assert checked == 72
