@@ -7,8 +7,9 @@
 // for a batch of same-shape matrices in one launch per GEMM phase.
 //
 // Layout.  Every matrix of the batch is held as the tall iterate T (n x m, n >= m;
-// W = T^T is the wide convention), bf16 row-major in a zero-padded workspace with
-// m, n rounded up to the 256 tile.  One iteration (a, b, c) is
+// W = T^T is the wide convention), bf16 in a zero-padded workspace with m, n
+// rounded up to the 256 tile, stored in 64 x 64 blocks (blk_off in ns_chain.h) so
+// that every K stage of the GEMMs reads contiguous memory.  One iteration (a, b, c) is
 //
 //   K1  A  = T^T T                  (m x m, K = n)  symmetric: upper tiles only
 //   K2  B' = b A + c A A + a I      (m x m, K = m)  symmetric: upper tiles only
@@ -96,19 +97,22 @@ static_assert(SMEM_BYTES <= 160 * 1024, "LDS ring and epilogue staging must fit 
 
 enum { EPI_STORE = 0, EPI_POLY = 1 };
 
+// P, Q and aux are block-layout matrices (blk_off) of p_rows, q_rows, aux_rows rows;
+// out / outT are block-layout when out_rows / outT_rows > 0, else row-major with
+// their leading dimension (the caller's output).
 struct GemmArgs {
-  const bf16* P; long long p_bs; int p_ld;      // rows i of C
-  const bf16* Q; long long q_bs; int q_ld;      // rows j of C
-  int K;                                         // multiple of TK, <= p_ld and q_ld
+  const bf16* P; long long p_bs; int p_rows;    // rows i of C
+  const bf16* Q; long long q_bs; int q_rows;    // rows j of C
+  int K;                                         // multiple of TK
   int tiles_m, tiles_n;                          // tiles per matrix
   int sym;                                       // upper-triangular tiles, mirrored stores
   int total_tiles;                               // over the batch
   int batch, rev;                                // rev: walk the batch from its last matrix
   float alpha, beta;                             // POLY: (b, c)
   float diag_add; int diag_lim;                  // POLY: + diag_add on C[i][i], i < diag_lim
-  const bf16* aux; long long aux_bs; int aux_ld; // POLY: A (indexed [i][j])
-  bf16* out; long long out_bs; int out_ld;       // C[i][j]   (may be null)
-  bf16* outT; long long outT_bs; int outT_ld;    // C[j][i]   (may be null)
+  const bf16* aux; long long aux_bs; int aux_rows; // POLY: A (indexed [i][j])
+  bf16* out; long long out_bs; int out_ld, out_rows;      // C[i][j]   (may be null)
+  bf16* outT; long long outT_bs; int outT_ld, outT_rows;  // C[j][i]   (may be null)
   int valid_i, valid_j;                          // stores limited to i < valid_i, j < valid_j
 };
 
@@ -167,18 +171,22 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Buffer descriptor of one operand tile.  Row-operand layout (TNL = 0): rows t*TILE..
-// +TILE-1 of a K-contiguous matrix.  K-major layout (TNL = 1): columns t*TILE..+TILE-1
-// of a matrix whose row k holds the operand's values for contraction index k.
+// Buffer descriptor of one operand tile of a block-layout matrix with R rows.
+// Row-operand layout (TNL = 0): rows t*TILE..+TILE-1 of a K-contiguous matrix; the
+// descriptor starts at their first K stage (4 consecutive blocks, 32 KB) and
+// covers the later stages, R * 128 bytes apart.  K-major layout (TNL = 1): columns
+// t*TILE..+TILE-1 of a matrix whose row k holds the operand's values for
+// contraction index k (R = K rows): 4 whole block columns, R * 128 bytes each.
 template <int TNL>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16* base, long long bs,
-                                                           int ld, int K, int b, int t) {
+                                                           int R, int K, int b, int t) {
   if (TNL) {
-    const bf16* p = base + (long long)b * bs + (long long)t * TILE;
-    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, K * ld * 2, 0x00020000);
+    const bf16* p = base + (long long)b * bs + (long long)(t * TILE) * R;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, TILE * R * 2, 0x00020000);
   }
-  const bf16* p = base + (long long)b * bs + (long long)(t * TILE) * ld;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, TILE * ld * 2, 0x00020000);
+  const bf16* p = base + (long long)b * bs + (long long)(t * TILE / CHAIN_BLK) * CHAIN_BLK * CHAIN_BLK;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (K / TK - 1) * R * ROWB + TILE * ROWB,
+                                           0x00020000);
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -242,6 +250,10 @@ void gemm_nt_bf16(GemmArgs g) {
   // transposing fragment reads (4 rows x 4 chunks per 16 lanes) over every bank.
   // Instruction q of wave w fills rows 8 w + 2 q and 8 w + 2 q + 1 (1 KB), so the
   // LDS destinations are the same as for the row-operand tiles.
+  // In global memory (block layout): a row-operand stage is 256 rows of 128 B, one
+  // after the other, and the next stage is R * 128 bytes further; a K-major stage is
+  // 64 rows of four 128-byte pieces, one per block column (R * 128 bytes apart), and
+  // the next stage is the next 8 KB block of each column.
   int boffP[LQ], boffQ[LQ];   // byte offsets within the tile
   if (TNL) {
     static_assert(TK / GEMM_WAVES == 2 * LQ && TILE * 2 == 32 * 16, "K-major loader layout");
@@ -249,8 +261,8 @@ void gemm_nt_bf16(GemmArgs g) {
     for (int q = 0; q < LQ; ++q) {
       const int r = (TK / GEMM_WAVES) * wave + 2 * q + (lane >> 5);
       const int c = (lane & 31) ^ (4 * (r & 3));
-      boffP[q] = (r * g.p_ld + c * 8) * 2;
-      boffQ[q] = (r * g.q_ld + c * 8) * 2;
+      boffP[q] = (c >> 3) * g.p_rows * ROWB + r * ROWB + (c & 7) * 16;
+      boffQ[q] = (c >> 3) * g.q_rows * ROWB + r * ROWB + (c & 7) * 16;
     }
   } else {
     const int lrow0 = (TILE / GEMM_WAVES) * wave + lane / CHUNKS;
@@ -259,12 +271,13 @@ void gemm_nt_bf16(GemmArgs g) {
     for (int q = 0; q < LQ; ++q) {
       const int r = lrow0 + LROWS * q;
       const int c = lslot ^ lds_swz(r);
-      boffP[q] = (r * g.p_ld + c * 8) * 2;
-      boffQ[q] = (r * g.q_ld + c * 8) * 2;
+      boffP[q] = r * ROWB + c * 16;
+      boffQ[q] = r * ROWB + c * 16;
     }
   }
-  // scalar byte offset of K stage k0: along the row, or down k0 rows (K-major)
-  const int kstepP = TNL ? g.p_ld * 2 : 2, kstepQ = TNL ? g.q_ld * 2 : 2;
+  // scalar byte offset of K stage k0 (a multiple of 64): k0 / 64 block columns
+  // further (row operands), or k0 rows down each block column (K-major)
+  const int kstepP = TNL ? ROWB : g.p_rows * 2, kstepQ = TNL ? ROWB : g.q_rows * 2;
   char* const lds_wave = smem + wave * (TILE / GEMM_WAVES) * ROWB;   // this wave's first row
 
 #define DMH_GLOAD(rp, rq, k0, st)                                                      \
@@ -334,8 +347,8 @@ void gemm_nt_bf16(GemmArgs g) {
   const int nk = g.K / TK;
   int b, ti, tj;
   decode_tile(g, lid, b, ti, tj);
-  __amdgpu_buffer_rsrc_t rP = tile_rsrc<TNL>(g.P, g.p_bs, g.p_ld, g.K, b, ti);
-  __amdgpu_buffer_rsrc_t rQ = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_ld, g.K, b, tj);
+  __amdgpu_buffer_rsrc_t rP = tile_rsrc<TNL>(g.P, g.p_bs, g.p_rows, g.K, b, ti);
+  __amdgpu_buffer_rsrc_t rQ = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_rows, g.K, b, tj);
   // Each tile walks its K stages starting at stage 3 (ti + tj) % nk and wrapping
   // around: the tiles that share an operand panel (same ti, or same tj) are then at
   // different K stages at any moment, so each line of a shared panel is fetched from
@@ -359,8 +372,8 @@ void gemm_nt_bf16(GemmArgs g) {
     const bool more = nlid < lend;
     int nb = b, nti = ti, ntj = tj;
     if (more) decode_tile(g, nlid, nb, nti, ntj);
-    const __amdgpu_buffer_rsrc_t rPn = tile_rsrc<TNL>(g.P, g.p_bs, g.p_ld, g.K, nb, nti);
-    const __amdgpu_buffer_rsrc_t rQn = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_ld, g.K, nb, ntj);
+    const __amdgpu_buffer_rsrc_t rPn = tile_rsrc<TNL>(g.P, g.p_bs, g.p_rows, g.K, nb, nti);
+    const __amdgpu_buffer_rsrc_t rQn = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_rows, g.K, nb, ntj);
 
     // Main loop of one tile, software-pipelined at two levels:
     //  * LDS ring: stage kt+1 is in flight while stage kt is consumed;
@@ -467,7 +480,16 @@ void gemm_nt_bf16(GemmArgs g) {
       const bool diag = g.sym && ti == tj;
       bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
       bf16* outtb = g.outT && !diag ? g.outT + (long long)b * g.outT_bs : nullptr;
-      const bool al_out = (g.out_ld & 7) == 0, al_outT = (g.outT_ld & 7) == 0;
+      const bool al_out = g.out_rows > 0 || (g.out_ld & 7) == 0;
+      const bool al_outT = g.outT_rows > 0 || (g.outT_ld & 7) == 0;
+      // element offsets of C[i][j..j+7] and C^T[j][i..i+7] (8 consecutive bf16 either way:
+      // blocks are 64 wide and the chunks 8-aligned)
+      auto out_off = [&](int i, int j) {
+        return g.out_rows > 0 ? blk_off(i, j, g.out_rows) : (long long)i * g.out_ld + j;
+      };
+      auto outT_off = [&](int j, int i) {
+        return g.outT_rows > 0 ? blk_off(j, i, g.outT_rows) : (long long)j * g.outT_ld + i;
+      };
       const bf16* auxb = EPI == EPI_POLY ? g.aux + (long long)b * g.aux_bs : nullptr;
       // one store per 16-byte chunk when the wave's 128 x 64 block is whole and
       // aligned: the epilogue then issues a known number of memory instructions
@@ -484,7 +506,7 @@ void gemm_nt_bf16(GemmArgs g) {
         for (int v = 0; v < 4; ++v) {
           const int u = lane + 64 * v;
           const int gi = wi0 + 32 * bi + (u >> 3), gj = wj0 + 8 * (u & 7);
-          av[bi][v] = *(const bf16x8*)(auxb + (long long)gi * g.aux_ld + gj);
+          av[bi][v] = *(const bf16x8*)(auxb + blk_off(gi, gj, g.aux_rows));
         }
       };
       if (EPI == EPI_POLY) {
@@ -529,7 +551,7 @@ void gemm_nt_bf16(GemmArgs g) {
           if (outb && gi < g.valid_i) {
             unsigned mask = 0xffu;
             if (gj + 8 > g.valid_j) mask = gj >= g.valid_j ? 0u : (1u << (g.valid_j - gj)) - 1u;
-            if (mask) store8(outb + (long long)gi * g.out_ld + gj, val, mask, al_out);
+            if (mask) store8(outb + out_off(gi, gj), val, mask, al_out);
           }
         }
         // phase 2b: POLY's stored values back into acc (the inverse of phase 1)
@@ -590,8 +612,7 @@ void gemm_nt_bf16(GemmArgs g) {
               if (gi + 8 > g.valid_i) mask = gi >= g.valid_i ? 0u : (1u << (g.valid_i - gi)) - 1u;
               if (mask) {
                 const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
-                store8(outtb + (long long)gj * g.outT_ld + gi, __builtin_bit_cast(bf16x8, wv), mask,
-                       al_outT);
+                store8(outtb + outT_off(gj, gi), __builtin_bit_cast(bf16x8, wv), mask, al_outT);
               }
             }
           }
@@ -688,7 +709,7 @@ __global__ __launch_bounds__(256) void entry_pack(InView v, int in_tall, int sca
   bf16* Tb = T + (long long)b * np * mp;
   for (int rr = ty; rr < 64; rr += 4) {
     const float xt = scale_mode ? tile[rr][tx] / scale : tile[rr][tx];
-    Tb[(long long)(i0 + rr) * mp + j0 + tx] = f2bf(xt);
+    Tb[blk_off(i0 + rr, j0 + tx, np)] = f2bf(xt);
   }
 }
 
@@ -701,7 +722,7 @@ __global__ __launch_bounds__(256) void copy_out(const bf16* T, int np, int mp, i
     int i, j;
     if (out_tall) { i = (int)(e / m); j = (int)(e - (long long)i * m); }
     else { j = (int)(e / n); i = (int)(e - (long long)j * n); }
-    out[(long long)b * total + e] = T[(long long)b * np * mp + (long long)i * mp + j];
+    out[(long long)b * total + e] = T[(long long)b * np * mp + blk_off(i, j, np)];
   }
 }
 
@@ -788,31 +809,31 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     // K1: A = W W^T = T^T T, with both operands read K-major from T (row k of T
     // holds column k of W)
     GemmArgs g1{};
-    g1.P = Tc; g1.p_bs = (long long)d.np * d.mp; g1.p_ld = d.mp;
-    g1.Q = Tc; g1.q_bs = g1.p_bs; g1.q_ld = d.mp;
+    g1.P = Tc; g1.p_bs = (long long)d.np * d.mp; g1.p_rows = d.np;
+    g1.Q = Tc; g1.q_bs = g1.p_bs; g1.q_rows = d.np;
     g1.K = d.np; g1.tiles_m = tm; g1.tiles_n = tm; g1.sym = 1;
-    g1.out = Am; g1.out_bs = (long long)d.mp * d.mp; g1.out_ld = d.mp;
-    g1.outT = Am; g1.outT_bs = g1.out_bs; g1.outT_ld = d.mp;
+    g1.out = Am; g1.out_bs = (long long)d.mp * d.mp; g1.out_rows = d.mp;
+    g1.outT = Am; g1.outT_bs = g1.out_bs; g1.outT_rows = d.mp;
     g1.valid_i = d.mp; g1.valid_j = d.mp;
     g1.rev = rev; rev ^= 1;
     if ((rc = launch_gemm<EPI_STORE, 1>(g1, batch, stream, "ns K1 (T^T T)"))) return rc;
     // K2: B = b A + c A A
     GemmArgs g2 = g1;
-    g2.P = Am; g2.p_bs = (long long)d.mp * d.mp; g2.p_ld = d.mp;
-    g2.Q = Am; g2.q_bs = g2.p_bs; g2.q_ld = d.mp;
+    g2.P = Am; g2.p_bs = (long long)d.mp * d.mp; g2.p_rows = d.mp;
+    g2.Q = Am; g2.q_bs = g2.p_bs; g2.q_rows = d.mp;
     g2.K = d.mp;
     g2.alpha = bcoef; g2.beta = c; g2.diag_add = a; g2.diag_lim = d.m;
-    g2.aux = Am; g2.aux_bs = g2.p_bs; g2.aux_ld = d.mp;
+    g2.aux = Am; g2.aux_bs = g2.p_bs; g2.aux_rows = d.mp;
     g2.out = Bm; g2.outT = Bm;
     g2.rev = rev; rev ^= 1;
     if ((rc = launch_gemm<EPI_POLY, 0>(g2, batch, stream, "ns K2 (bA + cA^2 + aI)"))) return rc;
     // K3: T' = T B' (the final iterate in the caller's orientation)
     GemmArgs g3{};
-    g3.P = Tc; g3.p_bs = (long long)d.np * d.mp; g3.p_ld = d.mp;
-    g3.Q = Bm; g3.q_bs = (long long)d.mp * d.mp; g3.q_ld = d.mp;
+    g3.P = Tc; g3.p_bs = (long long)d.np * d.mp; g3.p_rows = d.np;
+    g3.Q = Bm; g3.q_bs = (long long)d.mp * d.mp; g3.q_rows = d.mp;
     g3.K = d.mp; g3.tiles_m = tn; g3.tiles_n = tm; g3.sym = 0;
     if (!last) {
-      g3.out = Tn; g3.out_bs = g3.p_bs; g3.out_ld = d.mp;
+      g3.out = Tn; g3.out_bs = g3.p_bs; g3.out_rows = d.np;
       g3.valid_i = d.np; g3.valid_j = d.mp;
     } else if (orient_tall) {
       g3.out = outp; g3.out_bs = (long long)d.n * d.m; g3.out_ld = d.m;

@@ -1190,8 +1190,9 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
 //      = A / d - sum_{t<k} U[i][t] (cw_t / d - cr_t) V[j][t]
 // per 64 x 64 tile, rank-k update on VALU (k <= 63), fp32.  Outputs, any subset:
 //   X0   (B, n, m) bf16 or fp32, the API tensor
-//   T, W the NS chain's packed bf16 operands (np x mp and its transpose, zero
-//        outside n x m), so the chain can start without its entry pass
+//   T, W the NS chain's packed bf16 operands (T: np x mp in the chain's 64 x 64
+//        block layout, W: its transpose, row-major; zero outside n x m), so the
+//        chain can start without its entry pass
 // ---------------------------------------------------------------------------
 constexpr int DR_ROWS = 64, DR_COLS = 128;
 constexpr int DR_KC = 16;   // head columns staged per chunk
@@ -1320,8 +1321,8 @@ __global__ __launch_bounds__(256) void deflate_restore(
         }
       }
     }
-    if (T && gi < np && gj < mp)
-      *(bf16x4*)(T + (long long)b * np * mp + (long long)gi * mp + gj) = o;
+    if (T && gi < np && gj < mp)   // the chain's block layout (blk_off)
+      *(bf16x4*)(T + (long long)b * np * mp + blk_off(gi, gj, np)) = o;
     if (W) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) sm.tw[c4 + c][il] = o[c];

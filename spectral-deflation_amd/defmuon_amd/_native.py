@@ -76,11 +76,13 @@ class NativeError(RuntimeError):
     pass
 
 
-def load(path=LIB_PATH):
-    """Load (once) and return the library handle."""
+def load(path=None):
+    """Load (once) and return the library handle (from `path`, else the module's
+    LIB_PATH as it is at the first call)."""
     global _lib
     if _lib is not None:
         return _lib
+    path = path or LIB_PATH
     if not os.path.exists(path):
         raise NativeError(
             f"HIP library not built: {path} is missing.  Build it with "
