@@ -108,6 +108,7 @@ struct GemmArgs {
   int sym;                                       // upper-triangular tiles, mirrored stores
   int total_tiles;                               // over the batch
   int batch, rev;                                // rev: walk the batch from its last matrix
+  int kspread;                                   // K walk starts at stage kspread (ti + tj) mod nk
   float alpha, beta;                             // POLY: (b, c)
   float diag_add; int diag_lim;                  // POLY: + diag_add on C[i][i], i < diag_lim
   const bf16* aux; long long aux_bs; int aux_rows; // POLY: A (indexed [i][j])
@@ -349,15 +350,14 @@ void gemm_nt_bf16(GemmArgs g) {
   decode_tile(g, lid, b, ti, tj);
   __amdgpu_buffer_rsrc_t rP = tile_rsrc<TNL>(g.P, g.p_bs, g.p_rows, g.K, b, ti);
   __amdgpu_buffer_rsrc_t rQ = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_rows, g.K, b, tj);
-  // Each tile walks its K stages starting at stage 3 (ti + tj) % nk and wrapping
-  // around: the tiles that share an operand panel (same ti, or same tj) are then at
-  // different K stages at any moment, so each line of a shared panel is fetched from
-  // memory by the first of them and found in L2 by the others a few stages later,
-  // instead of all of them waiting on the same miss (a spread of 3 stages per step of
-  // ti + tj measured best among 1, 2, 3 and 4; -1.9% to -4% of the chain time).  The
-  // offset depends on the tile alone, so a matrix gets the same result whatever batch
-  // it is in.
-  int kofs = (3 * (ti + tj)) % nk;
+  // Each tile walks its K stages starting at stage kspread (ti + tj) % nk and
+  // wrapping around: the tiles that share an operand panel (same ti, or same tj) are
+  // then at different K stages at any moment, so each line of a shared panel is
+  // fetched from memory by the first of them and found in L2 by the others a few
+  // stages later, instead of all of them waiting on the same miss.  The best spread
+  // differs by product (measured over 0..6: K1 1, K2 0, K3 2).  The offset depends
+  // on the tile alone, so a matrix gets the same result whatever batch it is in.
+  int kofs = (g.kspread * (ti + tj)) % nk;
   DMH_GLOAD(rP, rQ, kofs * TK, 0);
 
   char* const stg = smem + RING_BYTES + wave * EPI_WAVE_BYTES;   // this wave's staging
@@ -437,7 +437,7 @@ void gemm_nt_bf16(GemmArgs g) {
     // Last stage: the next tile's first stage goes into the free slot (it held stage
     // nk-2, or the previous tile's last stage, both consumed before a barrier) and
     // stays in flight under the epilogue.
-    const int nkofs = (3 * (nti + ntj)) % nk;
+    const int nkofs = (g.kspread * (nti + ntj)) % nk;
     if (more) DMH_GLOAD(rPn, rQn, nkofs * TK, s_cur ^ 1);
     __builtin_amdgcn_s_setprio(1);
     {
@@ -816,6 +816,7 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     g1.outT = Am; g1.outT_bs = g1.out_bs; g1.outT_rows = d.mp;
     g1.valid_i = d.mp; g1.valid_j = d.mp;
     g1.rev = rev; rev ^= 1;
+    g1.kspread = 1;
     if ((rc = launch_gemm<EPI_STORE, 1>(g1, batch, stream, "ns K1 (T^T T)"))) return rc;
     // K2: B = b A + c A A
     GemmArgs g2 = g1;
@@ -826,6 +827,7 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     g2.aux = Am; g2.aux_bs = g2.p_bs; g2.aux_rows = d.mp;
     g2.out = Bm; g2.outT = Bm;
     g2.rev = rev; rev ^= 1;
+    g2.kspread = 0;
     if ((rc = launch_gemm<EPI_POLY, 0>(g2, batch, stream, "ns K2 (bA + cA^2 + aI)"))) return rc;
     // K3: T' = T B' (the final iterate in the caller's orientation)
     GemmArgs g3{};
@@ -843,6 +845,7 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
       g3.valid_i = d.n; g3.valid_j = d.m;
     }
     g3.rev = rev; rev ^= 1;
+    g3.kspread = 2;
     if ((rc = launch_gemm<EPI_STORE, 0>(g3, batch, stream, "ns K3 (T B')"))) return rc;
     bf16* t = Tc; Tc = Tn; Tn = t;
   }
