@@ -647,69 +647,146 @@ __device__ __forceinline__ float load_in(const InView& v, int b, int r, int c) {
   return bf2f(((const bf16*)v.x)[off]);
 }
 
+// Sum of squares of one matrix of the input, NORM_CHUNKS partials per matrix (fp64,
+// per element), one workgroup per partial.  When the matrix's rows are contiguous
+// and back to back (column stride 1, row stride = cols) the matrix is one run of
+// rows * cols elements, read in 16-byte loads from its first 16-byte boundary on;
+// otherwise each workgroup takes a range of rows and reads them element by element.
 __global__ __launch_bounds__(256) void entry_norm_partials(InView v, double* partials) {
-  const int b = blockIdx.y, chunk = blockIdx.x;
-  const long long total = (long long)v.rows * v.cols;
-  const long long per = (total + NORM_CHUNKS - 1) / NORM_CHUNKS;
-  const long long lo = chunk * per;
-  const long long hi = lo + per < total ? lo + per : total;
+  const int b = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
   double s = 0.0;
-  for (long long e = lo + threadIdx.x; e < hi; e += blockDim.x) {
-    const int r = (int)(e / v.cols), c = (int)(e - (long long)r * v.cols);
-    const float x = load_in(v, b, r, c);
-    s += (double)x * (double)x;
+  if (v.cs == 1 && v.rs == v.cols) {
+    const long long total = (long long)v.rows * v.cols;
+    const long long per = (total + NORM_CHUNKS - 1) / NORM_CHUNKS;
+    const long long lo = (long long)chunk * per;
+    const long long hi = lo + per < total ? lo + per : total;
+    const int vec = v.dtype == 0 ? 4 : 8;   // elements per 16 bytes
+    const char* base = (const char*)v.x + ((long long)b * v.bs) * (v.dtype == 0 ? 4 : 2);
+    const int esz = v.dtype == 0 ? 4 : 2;
+    // first element of [lo, hi) on a 16-byte boundary
+    long long a = lo + (long long)((16 - (((uintptr_t)(base + lo * esz)) & 15)) & 15) / esz;
+    if (a > hi) a = hi;
+    const long long nvec = (hi - a) / vec;
+    const long long tail = a + nvec * vec;
+    for (long long e = lo + tid; e < a; e += 256) {
+      const float x = v.dtype == 0 ? ((const float*)base)[e] : bf2f(((const bf16*)base)[e]);
+      s += (double)x * (double)x;
+    }
+    if (v.dtype == 0) {
+      const float4* p4 = (const float4*)(base + a * 4);
+      for (long long q = tid; q < nvec; q += 256) {
+        const float4 x = p4[q];
+        s += (double)x.x * (double)x.x + (double)x.y * (double)x.y +
+             (double)x.z * (double)x.z + (double)x.w * (double)x.w;
+      }
+    } else {
+      const bf16x8* p8 = (const bf16x8*)(base + a * 2);
+      for (long long q = tid; q < nvec; q += 256) {
+        const bf16x8 x = p8[q];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s += (double)bf2f(x[k]) * (double)bf2f(x[k]);
+      }
+    }
+    for (long long e = tail + tid; e < hi; e += 256) {
+      const float x = v.dtype == 0 ? ((const float*)base)[e] : bf2f(((const bf16*)base)[e]);
+      s += (double)x * (double)x;
+    }
+  } else {
+    const int rpc = (v.rows + NORM_CHUNKS - 1) / NORM_CHUNKS;
+    const int r0 = chunk * rpc, r1 = r0 + rpc < v.rows ? r0 + rpc : v.rows;
+    for (int r = r0; r < r1; ++r)
+      for (int c = tid; c < v.cols; c += 256) {
+        const float x = load_in(v, b, r, c);
+        s += (double)x * (double)x;
+      }
   }
   __shared__ double red[256];
-  red[threadIdx.x] = s;
+  red[tid] = s;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    if (tid < w) red[tid] += red[tid + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) partials[b * NORM_CHUNKS + chunk] = red[0];
+  if (tid == 0) partials[b * NORM_CHUNKS + chunk] = red[0];
 }
 
-// Pack 64x64 tiles of T (i < np rows, j < mp cols).  in_tall: the input is T
-// (rows = n); otherwise it is W = T^T (rows = m) and is transposed on the way.
-// scale_mode: 0 none, 1: 1/(||x||+1e-7), 2: 1/(1.01||x||+1e-7).
+// Pack 64x64 tiles of T (i < np rows, j < mp cols) into the chain's block layout.
+// in_tall: the input is T (rows = n); otherwise it is W = T^T (rows = m) and is
+// transposed on the way through LDS.  scale_mode: 0 none, 1: x / (||x|| + 1e-7),
+// 2: x / (1.01 ||x|| + 1e-7), one fp32 division and one bf16 rounding per element.
+// fp32 input whose rows are contiguous and 16-byte aligned is read 4 elements at a
+// time (16 lanes per 64-column row); anything else element by element.
 __global__ __launch_bounds__(256) void entry_pack(InView v, int in_tall, int scale_mode,
                                                   const double* partials, int n, int m,
                                                   int np, int mp, bf16* T) {
   __shared__ float tile[64][65];
-  const int b = blockIdx.z;
+  const int b = blockIdx.z, tid = threadIdx.x;
   const int i0 = blockIdx.y * 64, j0 = blockIdx.x * 64;
-  float scale = 1.f;
+  float den = 1.f;
   if (scale_mode) {
-    __shared__ float s_scale;
-    if (threadIdx.x == 0) {
+    __shared__ float s_den;
+    if (tid == 0) {
       double s = 0.0;
       for (int c = 0; c < NORM_CHUNKS; ++c) s += partials[b * NORM_CHUNKS + c];
       const float nrm = (float)sqrt(s);
-      const float den = scale_mode == 2 ? nrm * 1.01f + 1e-7f : nrm + 1e-7f;
-      s_scale = den;
+      s_den = scale_mode == 2 ? nrm * 1.01f + 1e-7f : nrm + 1e-7f;
     }
     __syncthreads();
-    scale = s_scale;
+    den = s_den;
   }
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  // load in the input's natural orientation (coalesced along its columns)
-  for (int rr = ty; rr < 64; rr += 4) {
-    float x = 0.f;
-    if (in_tall) {
-      const int i = i0 + rr, j = j0 + tx;
-      if (i < n && j < m) x = load_in(v, b, i, j);
-      tile[rr][tx] = x;
-    } else {
-      const int j = j0 + rr, i = i0 + tx;   // W[j][i]
-      if (i < n && j < m) x = load_in(v, b, j, i);
-      tile[tx][rr] = x;
-    }
-  }
-  __syncthreads();
   bf16* Tb = T + (long long)b * np * mp;
-  for (int rr = ty; rr < 64; rr += 4) {
-    const float xt = scale_mode ? tile[rr][tx] / scale : tile[rr][tx];
-    Tb[blk_off(i0 + rr, j0 + tx, np)] = f2bf(xt);
+  const float* xf = (const float*)v.x;
+  const bool vec = v.dtype == 0 && v.cs == 1 && (v.rs & 3) == 0 && (v.bs & 3) == 0 &&
+                   (((uintptr_t)v.x) & 15) == 0;
+  // 4 consecutive elements of row r, columns c..c+3 of the input (zero outside
+  // rows x cols)
+  auto load4 = [&](int r, int c, int rows, int cols) {
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r >= rows) return x;
+    if (vec && c + 3 < cols) {
+      x = *(const float4*)(xf + (long long)b * v.bs + (long long)r * v.rs + c);
+    } else {
+      if (c + 0 < cols) x.x = load_in(v, b, r, c + 0);
+      if (c + 1 < cols) x.y = load_in(v, b, r, c + 1);
+      if (c + 2 < cols) x.z = load_in(v, b, r, c + 2);
+      if (c + 3 < cols) x.w = load_in(v, b, r, c + 3);
+    }
+    return x;
+  };
+  const int cq = (tid & 15) * 4;   // 4 columns of the tile
+  const int rr0 = tid >> 4;        // rows rr0 + 16 k
+  if (in_tall) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = i0 + rr0 + 16 * k;
+      float4 x = load4(i, j0 + cq, n, m);
+      if (scale_mode) { x.x = x.x / den; x.y = x.y / den; x.z = x.z / den; x.w = x.w / den; }
+      bf16x4 o;
+      o[0] = f2bf(x.x); o[1] = f2bf(x.y); o[2] = f2bf(x.z); o[3] = f2bf(x.w);
+      *(bf16x4*)(Tb + blk_off(i, j0 + cq, np)) = o;
+    }
+  } else {
+    // input rows j0.. (columns of T), columns i0.. (rows of T): W[j][i] -> tile[j][i]
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int jj = rr0 + 16 * k;
+      const float4 x = load4(j0 + jj, i0 + cq, m, n);
+      tile[jj][cq + 0] = x.x; tile[jj][cq + 1] = x.y; tile[jj][cq + 2] = x.z; tile[jj][cq + 3] = x.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int ii = rr0 + 16 * k;
+      float y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        y[q] = tile[cq + q][ii];
+        if (scale_mode) y[q] = y[q] / den;
+      }
+      bf16x4 o;
+      o[0] = f2bf(y[0]); o[1] = f2bf(y[1]); o[2] = f2bf(y[2]); o[3] = f2bf(y[3]);
+      *(bf16x4*)(Tb + blk_off(i0 + ii, j0 + cq, np)) = o;
+    }
   }
 }
 
