@@ -177,6 +177,28 @@ int dmh_momentum_stack(dmh_stream_t stream, const dmh_glue_param* params, int co
 int dmh_apply_update(dmh_stream_t stream, const dmh_glue_param* params, int count,
                      const void* ustack);
 
+/* ---- AdamW backup for the non-Muon parameters (one launch per group) ------------
+ * Replaces the per-parameter loop of muon.py:408-436 (buf1.lerp_(g, 1 - beta1);
+ * buf2.lerp_(g.square(), 1 - beta2); g = buf1 / (eps + buf2.sqrt());
+ * p.mul_(1 - lr*wd); p.add_(g, alpha=-lr/scale)) with the same fp32 operations in
+ * the same order.  `table` (device memory, `count` entries) lists the group's
+ * parameters; `chunk_start` (device memory, count + 1 ints) gives each parameter's
+ * first chunk of dmh_adamw_chunks-sized work, chunk_start[count] = nchunks.  The
+ * caller keeps both arrays (the tensors do not move between steps), so a step
+ * allocates and copies nothing.  w1 = 1 - beta1, w2 = 1 - beta2, decay = 1 - lr*wd,
+ * alpha = -lr/scale with scale the bias correction of the (common) step count. */
+typedef struct {
+  float* param;        /* updated in place */
+  const float* grad;
+  float* moment1;      /* updated in place */
+  float* moment2;      /* updated in place */
+  long long numel;
+} dmh_adamw_param;
+int dmh_adamw_chunks(long long numel);
+int dmh_adamw_step(dmh_stream_t stream, const dmh_adamw_param* table, int count,
+                   const int* chunk_start, int nchunks, float w1, float w2, float eps,
+                   float decay, float alpha);
+
 #ifdef __cplusplus
 }
 #endif

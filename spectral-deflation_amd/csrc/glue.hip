@@ -77,21 +77,51 @@ __device__ __forceinline__ float decayed(float p, float decay) {
   return p * decay;                             // p.mul_(1 - lr wd)
 }
 
+// 16-byte access is possible for a parameter when its rows, its tall block's rows
+// and every base address are 4-element aligned (then a whole 64 x 64 tile is read and
+// written 4 elements per lane)
+__device__ __forceinline__ bool glue_vec(const GlueParam& d, const BlockGeom& g, const void* other) {
+  return (d.cols & 3) == 0 && (g.m & 3) == 0 && (g.n & 3) == 0 && (d.offset & 3) == 0 &&
+         ((((uintptr_t)d.grad) | ((uintptr_t)d.buf) | ((uintptr_t)d.param) |
+           ((uintptr_t)other)) & 15) == 0;
+}
+
 // One workgroup per 64 x 64 tile of a tall block (grid-stride over the tiles of
 // parameter blockIdx.y).  Without transpose both sides are row-contiguous; with it
 // the tile goes through LDS so that the parameter side is read along its rows and
-// the stack side written along its rows.
+// the stack side written along its rows.  Whole tiles of aligned parameters move 4
+// elements per lane (16 lanes per 64-element row); edge tiles go element by element.
 __global__ __launch_bounds__(256) void momentum_stack(GlueArgs a) {
   __shared__ float t[GT][GT + 1];
   const GlueParam& d = a.p[blockIdx.y];
   const BlockGeom g = geom(d);
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c4 = (threadIdx.x & 15) * 4, r16 = threadIdx.x >> 4;   // vector lanes
+  const bool vec = glue_vec(d, g, a.stack);
   for (int tile = blockIdx.x; tile < g.tiles; tile += gridDim.x) {
     const int k = tile / (g.tn * g.tm);
     const int rem = tile - k * g.tn * g.tm;
     const int i0 = (rem / g.tm) * GT, j0 = (rem % g.tm) * GT;   // in the tall block
     float* dst = a.stack + d.offset + (long long)k * g.n * g.m;
+    const bool whole = vec && i0 + GT <= g.n && j0 + GT <= g.m;
     if (!d.transpose) {
+      if (whole) {
+#pragma unroll
+        for (int q = 0; q < GT / 16; ++q) {
+          const int i = i0 + r16 + 16 * q, j = j0 + c4;
+          const long long src = (long long)(k * g.rb + i) * d.cols + j;
+          float4 b = *(const float4*)(d.buf + src);
+          const float4 gr = *(const float4*)(d.grad + src);
+          float4 v;
+          v.x = nesterov_step(gr.x, b.x, a.mu, a.nesterov);
+          v.y = nesterov_step(gr.y, b.y, a.mu, a.nesterov);
+          v.z = nesterov_step(gr.z, b.z, a.mu, a.nesterov);
+          v.w = nesterov_step(gr.w, b.w, a.mu, a.nesterov);
+          *(float4*)(d.buf + src) = b;
+          *(float4*)(dst + (long long)i * g.m + j) = v;
+        }
+        continue;
+      }
       for (int ii = ty; ii < GT; ii += 4) {
         const int i = i0 + ii, j = j0 + tx;
         if (i >= g.n || j >= g.m) continue;
@@ -104,6 +134,28 @@ __global__ __launch_bounds__(256) void momentum_stack(GlueArgs a) {
     } else {
       // tall (i, j) = parameter (k rb + j, i): parameter rows j0.., columns i0..
       __syncthreads();
+      if (whole) {
+#pragma unroll
+        for (int q = 0; q < GT / 16; ++q) {
+          const int rr = r16 + 16 * q;
+          const long long src = (long long)(k * g.rb + j0 + rr) * d.cols + i0 + c4;
+          float4 b = *(const float4*)(d.buf + src);
+          const float4 gr = *(const float4*)(d.grad + src);
+          t[rr][c4 + 0] = nesterov_step(gr.x, b.x, a.mu, a.nesterov);
+          t[rr][c4 + 1] = nesterov_step(gr.y, b.y, a.mu, a.nesterov);
+          t[rr][c4 + 2] = nesterov_step(gr.z, b.z, a.mu, a.nesterov);
+          t[rr][c4 + 3] = nesterov_step(gr.w, b.w, a.mu, a.nesterov);
+          *(float4*)(d.buf + src) = b;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < GT / 16; ++q) {
+          const int ii = r16 + 16 * q;
+          *(float4*)(dst + (long long)(i0 + ii) * g.m + j0 + c4) =
+              make_float4(t[c4][ii], t[c4 + 1][ii], t[c4 + 2][ii], t[c4 + 3][ii]);
+        }
+        continue;
+      }
       for (int rr = ty; rr < GT; rr += 4) {
         const int pr = j0 + rr, pc = i0 + tx;
         if (pr < g.m && pc < g.n) {
@@ -127,12 +179,31 @@ __global__ __launch_bounds__(256) void apply_update(GlueArgs a) {
   const GlueParam& d = a.p[blockIdx.y];
   const BlockGeom g = geom(d);
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c4 = (threadIdx.x & 15) * 4, r16 = threadIdx.x >> 4;   // vector lanes
+  // (bf16 updates: 4 elements are 8 bytes)
+  const bool vec = glue_vec(d, g, nullptr) && (((uintptr_t)a.ustack) & 7) == 0;
   for (int tile = blockIdx.x; tile < g.tiles; tile += gridDim.x) {
     const int k = tile / (g.tn * g.tm);
     const int rem = tile - k * g.tn * g.tm;
     const int i0 = (rem / g.tm) * GT, j0 = (rem % g.tm) * GT;
     const bf16* src = a.ustack + d.offset + (long long)k * g.n * g.m;
+    const bool whole = vec && i0 + GT <= g.n && j0 + GT <= g.m;
     if (!d.transpose) {
+      if (whole) {
+#pragma unroll
+        for (int q = 0; q < GT / 16; ++q) {
+          const int i = i0 + r16 + 16 * q, j = j0 + c4;
+          const long long pi = (long long)(k * g.rb + i) * d.cols + j;
+          float4 pv = *(const float4*)(d.param + pi);
+          const bf16x4 u = *(const bf16x4*)(src + (long long)i * g.m + j);
+          pv.x = fmaf(d.alpha, bf2f(u[0]), decayed(pv.x, d.decay));
+          pv.y = fmaf(d.alpha, bf2f(u[1]), decayed(pv.y, d.decay));
+          pv.z = fmaf(d.alpha, bf2f(u[2]), decayed(pv.z, d.decay));
+          pv.w = fmaf(d.alpha, bf2f(u[3]), decayed(pv.w, d.decay));
+          *(float4*)(d.param + pi) = pv;
+        }
+        continue;
+      }
       for (int ii = ty; ii < GT; ii += 4) {
         const int i = i0 + ii, j = j0 + tx;
         if (i >= g.n || j >= g.m) continue;
@@ -142,6 +213,31 @@ __global__ __launch_bounds__(256) void apply_update(GlueArgs a) {
       }
     } else {
       __syncthreads();
+      if (whole) {
+#pragma unroll
+        for (int q = 0; q < GT / 16; ++q) {
+          const int ii = r16 + 16 * q;
+          const bf16x4 u = *(const bf16x4*)(src + (long long)(i0 + ii) * g.m + j0 + c4);
+          t[ii][c4 + 0] = bf2f(u[0]);
+          t[ii][c4 + 1] = bf2f(u[1]);
+          t[ii][c4 + 2] = bf2f(u[2]);
+          t[ii][c4 + 3] = bf2f(u[3]);
+        }
+        __syncthreads();
+        // parameter (k rb + j, i) = tall (i, j): parameter rows j0.., columns i0..
+#pragma unroll
+        for (int q = 0; q < GT / 16; ++q) {
+          const int rr = r16 + 16 * q;
+          const long long pi = (long long)(k * g.rb + j0 + rr) * d.cols + i0 + c4;
+          float4 pv = *(const float4*)(d.param + pi);
+          pv.x = fmaf(d.alpha, t[c4 + 0][rr], decayed(pv.x, d.decay));
+          pv.y = fmaf(d.alpha, t[c4 + 1][rr], decayed(pv.y, d.decay));
+          pv.z = fmaf(d.alpha, t[c4 + 2][rr], decayed(pv.z, d.decay));
+          pv.w = fmaf(d.alpha, t[c4 + 3][rr], decayed(pv.w, d.decay));
+          *(float4*)(d.param + pi) = pv;
+        }
+        continue;
+      }
       for (int ii = ty; ii < GT; ii += 4) {
         const int i = i0 + ii, j = j0 + tx;
         t[ii][tx] = (i < g.n && j < g.m) ? bf2f(src[(long long)i * g.m + j]) : 0.f;
@@ -206,11 +302,107 @@ static int check_params(const char* what, const GlueParam* ps, int count, int up
   return DMH_OK;
 }
 
+// ---------------------------------------------------------------------------
+// AdamW backup of the Muon optimizer (muon.py:408-436) for every non-Muon parameter
+// of a group in one launch.  Per element, the reference's torch ops in order, each
+// rounded to fp32:
+//     m1 <- lerp(m1, g, w1)           m1.lerp_(g, 1 - beta1)
+//     m2 <- lerp(m2, g * g, w2)       m2.lerp_(g.square(), 1 - beta2)
+//     u  <- m1 / (sqrt(m2) + eps)     buf1 / (eps + buf2.sqrt())
+//     p  <- p * decay                 p.mul_(1 - lr wd)
+//     p  <- p + alpha * u             p.add_(u, alpha=-lr / scale)
+// torch's lerp takes self + w (end - self) for |w| < 0.5, else end - (end - self)(1 - w),
+// each as one elementwise expression (a fused multiply-add); the division and the
+// square root are correctly rounded, as torch's are.
+// The parameter table and the chunk boundaries are device arrays the caller keeps
+// (the same tensors every step), so a launch copies and allocates nothing.
+// ---------------------------------------------------------------------------
+struct AdamwParam {
+  float* param;
+  const float* grad;
+  float* m1;
+  float* m2;
+  long long numel;
+};
+constexpr int ADAMW_CHUNK = 4096;   // elements per workgroup
+
+__device__ __forceinline__ float torch_lerp(float self, float end, float w) {
+  return fabsf(w) < 0.5f ? fmaf(w, end - self, self) : fmaf(-(end - self), 1.0f - w, end);
+}
+
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m1, float& m2, float w1,
+                                           float w2, float eps, float decay, float alpha) {
+#pragma clang fp contract(off)
+  m1 = torch_lerp(m1, g, w1);
+  const float g2 = g * g;
+  m2 = torch_lerp(m2, g2, w2);
+  const float u = m1 / (sqrtf(m2) + eps);
+  const float pd = p * decay;
+  p = fmaf(alpha, u, pd);
+}
+
+// chunk c of the group: parameter i with chunk_start[i] <= c < chunk_start[i + 1]
+__global__ __launch_bounds__(256) void adamw_step(const AdamwParam* __restrict__ tab, int count,
+                                                  const int* __restrict__ chunk_start, float w1,
+                                                  float w2, float eps, float decay, float alpha) {
+  const int c = blockIdx.x;
+  int lo = 0, hi = count;   // chunk_start[lo] <= c < chunk_start[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (chunk_start[mid] <= c) lo = mid; else hi = mid;
+  }
+  const AdamwParam d = tab[lo];
+  const long long e0 = (long long)(c - chunk_start[lo]) * ADAMW_CHUNK;
+  const long long e1 = e0 + ADAMW_CHUNK < d.numel ? e0 + ADAMW_CHUNK : d.numel;
+  const bool vec = ((((uintptr_t)d.param) | ((uintptr_t)d.grad) | ((uintptr_t)d.m1) |
+                     ((uintptr_t)d.m2)) & 15) == 0;
+  const long long ev = vec ? e0 + ((e1 - e0) & ~3LL) : e0;   // end of the 16-byte part
+  for (long long e = e0 + 4 * threadIdx.x; e < ev; e += 4 * 256) {
+    float4 p = *(const float4*)(d.param + e);
+    const float4 g = *(const float4*)(d.grad + e);
+    float4 a = *(const float4*)(d.m1 + e);
+    float4 v = *(const float4*)(d.m2 + e);
+    adamw_elem(p.x, g.x, a.x, v.x, w1, w2, eps, decay, alpha);
+    adamw_elem(p.y, g.y, a.y, v.y, w1, w2, eps, decay, alpha);
+    adamw_elem(p.z, g.z, a.z, v.z, w1, w2, eps, decay, alpha);
+    adamw_elem(p.w, g.w, a.w, v.w, w1, w2, eps, decay, alpha);
+    *(float4*)(d.param + e) = p;
+    *(float4*)(d.m1 + e) = a;
+    *(float4*)(d.m2 + e) = v;
+  }
+  for (long long e = ev + threadIdx.x; e < e1; e += 256) {
+    float p = d.param[e], a = d.m1[e], v = d.m2[e];
+    adamw_elem(p, d.grad[e], a, v, w1, w2, eps, decay, alpha);
+    d.param[e] = p;
+    d.m1[e] = a;
+    d.m2[e] = v;
+  }
+}
+
 }  // namespace dmh
 
 using namespace dmh;
 
 extern "C" {
+
+static_assert(sizeof(AdamwParam) == 40, "dmh_adamw_param layout");
+
+int dmh_adamw_chunks(long long numel) {
+  return numel <= 0 ? 0 : (int)((numel + ADAMW_CHUNK - 1) / ADAMW_CHUNK);
+}
+
+int dmh_adamw_step(hipStream_t stream, const void* table, int count, const int* chunk_start,
+                   int nchunks, float w1, float w2, float eps, float decay, float alpha) {
+  if (count == 0 || nchunks == 0) return DMH_OK;
+  if (count < 0 || nchunks < 0 || !table || !chunk_start) {
+    set_error("dmh_adamw_step: bad arguments (count=%d nchunks=%d)", count, nchunks);
+    return DMH_EINVAL;
+  }
+  hipLaunchKernelGGL(adamw_step, dim3(nchunks), dim3(256), 0, stream, (const AdamwParam*)table,
+                     count, chunk_start, w1, w2, eps, decay, alpha);
+  DMH_CHECK_LAUNCH("adamw_step");
+  return DMH_OK;
+}
 
 // layout of the descriptor the C header declares (dmh_glue_param)
 static_assert(sizeof(GlueParam) == 56, "dmh_glue_param layout");

@@ -57,6 +57,9 @@ _SIGS = {
                                          c_sz]),
     "dmh_momentum_stack": (c_int, [c_vp, c_vp, c_int, c_float, c_int, c_vp]),
     "dmh_apply_update": (c_int, [c_vp, c_vp, c_int, c_vp]),
+    "dmh_adamw_chunks": (c_int, [c_ll]),
+    "dmh_adamw_step": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_float, c_float, c_float,
+                               c_float, c_float]),
 }
 
 
@@ -351,3 +354,43 @@ def apply_update(params, ustack):
     _check(load().dmh_apply_update(_stream(ustack.device), ctypes.cast(arr, c_vp), len(params),
                                    _ptr(ustack)),
            "dmh_apply_update")
+
+
+class AdamwTable:
+    """The device-side parameter table and chunk boundaries of dmh_adamw_step for a
+    list of (param, grad, moment1, moment2) fp32 tensors.  It holds raw addresses:
+    reuse it only for tensors at the same addresses (`key`), in the same order.
+    The moments and parameters stay put between steps; gradients that come back at
+    the same addresses (torch's caching allocator) keep the table valid, otherwise
+    the caller builds a new one."""
+    __slots__ = ("key", "table", "chunks", "count", "nchunks")
+
+    def __init__(self, quads):
+        lib = load()
+        dev = quads[0][0].device
+        words, starts, total = [], [0], 0
+        for p, g, m1, m2 in quads:
+            words += [p.data_ptr(), g.data_ptr(), m1.data_ptr(), m2.data_ptr(), p.numel()]
+            total += lib.dmh_adamw_chunks(p.numel())
+            starts.append(total)
+        self.key = AdamwTable.key_of(quads)
+        # pinned staging so the copies are ordered on the stream without a host wait
+        self.table = torch.tensor(words, dtype=torch.int64).pin_memory().to(dev, non_blocking=True)
+        self.chunks = torch.tensor(starts, dtype=torch.int32).pin_memory().to(dev,
+                                                                              non_blocking=True)
+        self.count, self.nchunks = len(quads), total
+
+    @staticmethod
+    def key_of(quads):
+        return tuple(t.data_ptr() for q in quads for t in q)
+
+
+def adamw_step(tab, w1, w2, eps, decay, alpha):
+    """One AdamW step (muon.py:408-436) over every parameter of `tab` (AdamwTable),
+    enqueued on the current stream."""
+    if tab.count == 0:
+        return
+    _check(load().dmh_adamw_step(_stream(tab.table.device), _ptr(tab.table), tab.count,
+                                 _ptr(tab.chunks), tab.nchunks, float(w1), float(w2),
+                                 float(eps), float(decay), float(alpha)),
+           "dmh_adamw_step")

@@ -338,6 +338,43 @@ class Muon(torch.optim.Optimizer):
                 p.data.add_(u, alpha=-adjusted_lr)
         return True
 
+    # -- the AdamW backup as one library launch per group (FUSED_GLUE) ----------
+    def _adamw_fused(self, group, params, lr, weight_decay, beta1, beta2, eps):
+        """The AdamW loop below (muon.py:408-436) in one dmh_adamw_step launch per
+        distinct step count: the same fp32 operations per element, the moments
+        created and the step counts kept exactly as the loop does.  Returns False
+        (nothing done) when a tensor is not a contiguous fp32 GPU tensor."""
+        if not self.FUSED_GLUE:
+            return False
+        live = [p for p in params if p.grad is not None]
+        if not live:
+            return True
+        for p in live:
+            if any(not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous()
+                   for t in (p.data, p.grad)):
+                return False
+        by_step = {}
+        for p in live:
+            state = self.state[p]
+            if "step" not in state:
+                state["step"] = 0
+                state["moment1"] = torch.zeros_like(p.grad)
+                state["moment2"] = torch.zeros_like(p.grad)
+            state["step"] += 1
+            by_step.setdefault(state["step"], []).append(
+                (p.data, p.grad, state["moment1"], state["moment2"]))
+        cache = self.__dict__.setdefault("_adamw_tables", {})
+        for step, quads in by_step.items():
+            key = _native.AdamwTable.key_of(quads)
+            tab = cache.get(id(group), {}).get(step)
+            if tab is None or tab.key != key:
+                tab = _native.AdamwTable(quads)
+                cache[id(group)] = {step: tab}
+            scale = (1 - beta1 ** step) / (1 - beta2 ** step) ** 0.5
+            _native.adamw_step(tab, 1 - beta1, 1 - beta2, eps, 1 - lr * weight_decay,
+                               -lr / scale)
+        return True
+
     # -- step (muon.py:334-438) ------------------------------------------------
     def step(self, closure=None):
         loss = None
@@ -380,6 +417,8 @@ class Muon(torch.optim.Optimizer):
             params = [p for p in group["params"] if not self.state[p]["use_muon"]]
             beta1, beta2 = group["adamw_betas"]
             eps = group["adamw_eps"]
+            if self._adamw_fused(group, params, lr, weight_decay, beta1, beta2, eps):
+                params = []
             for p in params:
                 g = p.grad
                 if g is None:

@@ -272,3 +272,39 @@ def test_fused_glue_equals_torch_ops(muon_mod, nesterov):
         assert torch.equal(b0[k], b1[k]), ("momentum", k)
     for k in p0:
         assert torch.equal(p0[k], p1[k]), ("param", k, (p0[k] - p1[k]).abs().max().item())
+
+
+@pytest.mark.parametrize("betas", [(0.95, 0.95), (0.3, 0.6)])
+def test_fused_adamw_equals_torch_ops(muon_mod, betas):
+    """dmh_adamw_step (one launch for every non-Muon parameter) leaves the parameters
+    and both moments bit for bit where the reference's per-parameter loop
+    (muon.py:408-436) does, over three steps with weight decay.  betas (0.3, 0.6)
+    take torch's other lerp branch (weight >= 0.5); sizes that are not multiples of
+    4, and one spanning several 4096-element chunks, take the element tail and the
+    chunk boundaries."""
+    muon, _ = muon_mod
+    shapes = {"wte.weight": (1031, 67), "wpe.weight": (33, 7), "h.0.ln_1.weight": (5,),
+              "h.0.ln_1.bias": (4099,), "h.0.mlp.c_fc.bias": (3 * 4096 + 5,)}
+    results = {}
+    for fused in (False, True):
+        g = torch.Generator().manual_seed(3)
+        params = {k: torch.nn.Parameter((torch.randn(*v, generator=g) * 0.02).to(DEV))
+                  for k, v in shapes.items()}
+        grads = {k: (torch.randn(*v, generator=g) * 1e-2).to(DEV) for k, v in shapes.items()}
+        opt = muon.Muon(list(params.items()), lr=0.02, weight_decay=0.1, momentum=0.9,
+                        adamw_betas=betas, adamw_eps=1e-8, ns_steps=5, polar_method="ns5")
+        opt.FUSED_GLUE = fused
+        for step in range(3):
+            for k, p in params.items():
+                p.grad = grads[k] * (1.0 + 0.5 * step) - 0.003 * step
+            opt.step()
+        torch.cuda.synchronize()
+        results[fused] = ({k: v.detach().clone() for k, v in params.items()},
+                          {k: (opt.state[p]["moment1"].clone(), opt.state[p]["moment2"].clone(),
+                               opt.state[p]["step"]) for k, p in params.items()})
+    (p0, m0), (p1, m1) = results[False], results[True]
+    for k in shapes:
+        assert m0[k][2] == m1[k][2] == 3, k
+        assert torch.equal(m0[k][0], m1[k][0]), ("moment1", k)
+        assert torch.equal(m0[k][1], m1[k][1]), ("moment2", k)
+        assert torch.equal(p0[k], p1[k]), ("param", k, (p0[k] - p1[k]).abs().max().item())
