@@ -1219,6 +1219,74 @@ union RestoreLds {
   bf16 tw[DR_COLS][DR_ROWS + 8];         // tile of W = T^T
 };
 
+// Pieces shared by the restore pass and the explicit ||W||_F pass.  Thread tid
+// holds rows rw + 8 a (a = 0..7, rw = tid / 32) and columns c4 .. c4 + 3 (c4 =
+// 4 (tid % 32)) of a 64 x 128 tile; zeros outside n x m.
+__device__ __forceinline__ void dr_load_tile(const float* __restrict__ Ab, int n, int m, int i0,
+                                             int j0, int rw, int c4, bool vec,
+                                             float (&x)[8][4]) {
+#pragma unroll
+  for (int a = 0; a < 8; ++a) {
+    const int gi = i0 + rw + 8 * a, gj = j0 + c4;
+    if (gi < n && vec && gj + 3 < m) {
+      const float4 v = *(const float4*)&Ab[(long long)gi * m + gj];
+      x[a][0] = v.x; x[a][1] = v.y; x[a][2] = v.z; x[a][3] = v.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        x[a][c] = (gi < n && gj + c < m) ? Ab[(long long)gi * m + gj + c] : 0.f;
+    }
+  }
+}
+
+// Head columns t0 .. t0 + kc - 1 of the tile's U rows (64) and V rows (128), zero
+// past kc or the matrix: thread tid loads U[i0 + tid/16 + 16 q][t0 + tid%16], q < 4,
+// and V[j0 + tid/16 + 16 q][t0 + tid%16], q < 8, so each row's 16 floats are one
+// 64-byte piece.
+static_assert(DR_ROWS * DR_KC == 4 * 256 && DR_COLS * DR_KC == 8 * 256, "head chunk per thread");
+__device__ __forceinline__ void dr_load_head(const float* __restrict__ Ub,
+                                             const float* __restrict__ Vb, int n, int m, int i0,
+                                             int j0, int t0, int kc, int tid, float (&ur)[4],
+                                             float (&vr)[8]) {
+  const int t = tid % DR_KC, r0 = tid / DR_KC;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int gi = i0 + r0 + 16 * q;
+    ur[q] = (t < kc && gi < n) ? Ub[(long long)gi * RP + t0 + t] : 0.f;
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int gj = j0 + r0 + 16 * q;
+    vr[q] = (t < kc && gj < m) ? Vb[(long long)gj * RP + t0 + t] : 0.f;
+  }
+}
+
+__device__ __forceinline__ void dr_stage_head(RestoreLds& sm, const float (&ur)[4],
+                                              const float (&vr)[8], int tid) {
+  const int t = tid % DR_KC, r0 = tid / DR_KC;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sm.head.Us[r0 + 16 * q][t] = ur[q];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) sm.head.Vt[t][r0 + 16 * q] = vr[q];
+}
+
+// x -= sum_{t < kc} U[i][t0 + t] coef[t0 + t] V[j][t0 + t], t in order
+__device__ __forceinline__ void dr_apply_head(const RestoreLds& sm, const float* coef, int t0,
+                                              int kc, int rw, int c4, float (&x)[8][4]) {
+  for (int t = 0; t < kc; ++t) {
+    const float4 v = *(const float4*)&sm.head.Vt[t][c4];
+    const float ct = coef[t0 + t];
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+      const float u = sm.head.Us[rw + 8 * a][t] * ct;
+      x[a][0] = fmaf(-u, v.x, x[a][0]);
+      x[a][1] = fmaf(-u, v.y, x[a][1]);
+      x[a][2] = fmaf(-u, v.z, x[a][2]);
+      x[a][3] = fmaf(-u, v.w, x[a][3]);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void deflate_restore(
     const float* __restrict__ A, int n, int m, const float* __restrict__ U,
     const float* __restrict__ V, const int* __restrict__ kvec, const float* __restrict__ cw,
@@ -1232,6 +1300,16 @@ __global__ __launch_bounds__(256) void deflate_restore(
   const int i0 = blockIdx.y * DR_ROWS, j0 = blockIdx.x * DR_COLS;
   const int tid = threadIdx.x;
   const int k = kvec[b];
+  const int c4 = (tid & 31) * 4;      // 4 consecutive columns of the tile
+  const int rw = tid >> 5;            // rows rw + 8a, a = 0..7
+  const bool vec = (m & 3) == 0;
+  // Every global read of the tile goes out before the first wait: A (the bulk of the
+  // traffic), the first head chunk, and the norm partials of a flagged matrix
+  float x[8][4], ur[4], vr[8];
+  dr_load_tile(A + (long long)b * n * m, n, m, i0, j0, rw, c4, vec, x);
+  const float* Ub = U + (long long)b * n * RP;
+  const float* Vb = V + (long long)b * m * RP;
+  if (k > 0) dr_load_head(Ub, Vb, n, m, i0, j0, 0, min(DR_KC, k), tid, ur, vr);
   float d = dvec[b];
   if (wflag && wflag[b]) {
     // d from W itself: every workgroup sums the same partials in the same order
@@ -1249,25 +1327,6 @@ __global__ __launch_bounds__(256) void deflate_restore(
     d = (float)sqrt(wsum[0]) + 1e-7f;
     if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) dvec[b] = d;
   }
-  const float* Ab = A + (long long)b * n * m;
-  const int c4 = (tid & 31) * 4;      // 4 consecutive columns of the tile
-  const int rw = tid >> 5;            // rows rw + 8a, a = 0..7
-  const bool vec = (m & 3) == 0;
-  // A first (the bulk of the traffic), so its loads are in flight while the head
-  // coefficients and chunks are staged
-  float x[8][4];
-#pragma unroll
-  for (int a = 0; a < 8; ++a) {
-    const int gi = i0 + rw + 8 * a, gj = j0 + c4;
-    if (gi < n && vec && gj + 3 < m) {
-      const float4 v = *(const float4*)&Ab[(long long)gi * m + gj];
-      x[a][0] = v.x; x[a][1] = v.y; x[a][2] = v.z; x[a][3] = v.w;
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        x[a][c] = (gi < n && gj + c < m) ? Ab[(long long)gi * m + gj + c] : 0.f;
-    }
-  }
   if (tid < RP) coef[tid] = cw[b * RP + tid] / d - cr[b * RP + tid];
 #pragma unroll
   for (int a = 0; a < 8; ++a)
@@ -1275,30 +1334,11 @@ __global__ __launch_bounds__(256) void deflate_restore(
     for (int c = 0; c < 4; ++c) x[a][c] = x[a][c] / d;
   for (int t0 = 0; t0 < k; t0 += DR_KC) {
     const int kc = min(DR_KC, k - t0);
+    if (t0 > 0) dr_load_head(Ub, Vb, n, m, i0, j0, t0, kc, tid, ur, vr);
     __syncthreads();   // coef visible; the previous chunk consumed
-    for (int e = tid; e < DR_ROWS * DR_KC; e += 256) {   // U rows
-      const int rr = e / DR_KC, t = e % DR_KC;
-      const int gi = i0 + rr;
-      sm.head.Us[rr][t] = (t < kc && gi < n) ? U[((long long)b * n + gi) * RP + t0 + t] : 0.f;
-    }
-    for (int e = tid; e < DR_COLS * DR_KC; e += 256) {   // V rows, transposed
-      const int cc = e / DR_KC, t = e % DR_KC;
-      const int gj = j0 + cc;
-      sm.head.Vt[t][cc] = (t < kc && gj < m) ? V[((long long)b * m + gj) * RP + t0 + t] : 0.f;
-    }
+    dr_stage_head(sm, ur, vr, tid);
     __syncthreads();
-    for (int t = 0; t < kc; ++t) {
-      const float4 v = *(const float4*)&sm.head.Vt[t][c4];
-      const float ct = coef[t0 + t];
-#pragma unroll
-      for (int a = 0; a < 8; ++a) {
-        const float u = sm.head.Us[rw + 8 * a][t] * ct;
-        x[a][0] = fmaf(-u, v.x, x[a][0]);
-        x[a][1] = fmaf(-u, v.y, x[a][1]);
-        x[a][2] = fmaf(-u, v.z, x[a][2]);
-        x[a][3] = fmaf(-u, v.w, x[a][3]);
-      }
-    }
+    dr_apply_head(sm, coef, t0, kc, rw, c4, x);
   }
   if (W) __syncthreads();   // the head chunk is consumed before tw overwrites it
 #pragma unroll
@@ -1358,44 +1398,37 @@ __global__ __launch_bounds__(256) void w_norm_partials(
   const int tid = threadIdx.x;
   const int k = kvec[b];
   const float* Ab = A + (long long)b * n * m;
+  const float* Ub = U + (long long)b * n * RP;
+  const float* Vb = V + (long long)b * m * RP;
   const int c4 = (tid & 31) * 4, rw = tid >> 5;
+  const bool vec = (m & 3) == 0;
   const int tiles_x = (m + DR_COLS - 1) / DR_COLS, ntiles = wn_tiles(n, m);
   if (tid < RP) coef[tid] = cw[b * RP + tid];
   double sq = 0.0;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  // the next tile's A and first head chunk are requested before this tile's work
+  float x[8][4], ur[4], vr[8];
+  int tile = blockIdx.x;
+  if (tile < ntiles) {
     const int i0 = (tile / tiles_x) * DR_ROWS, j0 = (tile % tiles_x) * DR_COLS;
-    float x[8][4];
-#pragma unroll
-    for (int a = 0; a < 8; ++a)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
-        x[a][c] = (gi < n && gj < m) ? Ab[(long long)gi * m + gj] : 0.f;
-      }
+    dr_load_tile(Ab, n, m, i0, j0, rw, c4, vec, x);
+    if (k > 0) dr_load_head(Ub, Vb, n, m, i0, j0, 0, min(DR_KC, k), tid, ur, vr);
+  }
+  while (tile < ntiles) {
+    const int i0 = (tile / tiles_x) * DR_ROWS, j0 = (tile % tiles_x) * DR_COLS;
+    const int nt = tile + gridDim.x;
+    float xn[8][4], un[4], vn[8];
+    if (nt < ntiles) {
+      const int ni0 = (nt / tiles_x) * DR_ROWS, nj0 = (nt % tiles_x) * DR_COLS;
+      dr_load_tile(Ab, n, m, ni0, nj0, rw, c4, vec, xn);
+      if (k > 0) dr_load_head(Ub, Vb, n, m, ni0, nj0, 0, min(DR_KC, k), tid, un, vn);
+    }
     for (int t0 = 0; t0 < k; t0 += DR_KC) {
       const int kc = min(DR_KC, k - t0);
+      if (t0 > 0) dr_load_head(Ub, Vb, n, m, i0, j0, t0, kc, tid, ur, vr);
       __syncthreads();   // coef written; the previous chunk's readers done
-      for (int e = tid; e < DR_ROWS * DR_KC; e += 256) {
-        const int rr = e / DR_KC, t = e % DR_KC, gi = i0 + rr;
-        sm.head.Us[rr][t] = (t < kc && gi < n) ? U[((long long)b * n + gi) * RP + t0 + t] : 0.f;
-      }
-      for (int e = tid; e < DR_COLS * DR_KC; e += 256) {
-        const int cc = e / DR_KC, t = e % DR_KC, gj = j0 + cc;
-        sm.head.Vt[t][cc] = (t < kc && gj < m) ? V[((long long)b * m + gj) * RP + t0 + t] : 0.f;
-      }
+      dr_stage_head(sm, ur, vr, tid);
       __syncthreads();
-      for (int t = 0; t < kc; ++t) {
-        const float4 v = *(const float4*)&sm.head.Vt[t][c4];
-        const float ct = coef[t0 + t];
-#pragma unroll
-        for (int a = 0; a < 8; ++a) {
-          const float u = sm.head.Us[rw + 8 * a][t] * ct;
-          x[a][0] = fmaf(-u, v.x, x[a][0]);
-          x[a][1] = fmaf(-u, v.y, x[a][1]);
-          x[a][2] = fmaf(-u, v.z, x[a][2]);
-          x[a][3] = fmaf(-u, v.w, x[a][3]);
-        }
-      }
+      dr_apply_head(sm, coef, t0, kc, rw, c4, x);
     }
 #pragma unroll
     for (int a = 0; a < 8; ++a)
@@ -1404,6 +1437,15 @@ __global__ __launch_bounds__(256) void w_norm_partials(
         const int gi = i0 + rw + 8 * a, gj = j0 + c4 + c;
         if (gi < n && gj < m) sq += (double)x[a][c] * (double)x[a][c];
       }
+    tile = nt;
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) x[a][c] = xn[a][c];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ur[q] = un[q];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) vr[q] = vn[q];
   }
   red[tid] = sq;
   __syncthreads();
