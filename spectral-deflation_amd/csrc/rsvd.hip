@@ -16,6 +16,9 @@
 //   eig_gate            Jacobi eigen-decomposition of Bp Bp^T in LDS (fp64) -> s, Ub;
 //                       the deflation gate and the per-column deflate/restore weights
 //                       and d = ||A - U diag(s h) V^T||_F + 1e-7 from r x r quantities
+//   eig_head_gate       the same outputs for the clip / fused paths from the deflated
+//                       eigenpairs only: Householder tridiagonalisation, multisection
+//                       for the top kw eigenvalues, inverse iteration on the head
 //   deflate_restore     X0 = W / d + U diag(h / pad) V^T  -> bf16 / fp32, or straight
 //                       into the NS chain's packed operands (fused deflated polar)
 #include "common.h"
@@ -1185,6 +1188,523 @@ __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Gate eigen-decomposition for the clip and fused paths, where only the head
+// eigenpairs (the deflated directions) and the eigenvalues the gate compares are
+// needed; one 512-thread workgroup per matrix.
+//  1. Householder reduction of H = Bp Bp^T (r x r, fp64) to tridiagonal form
+//     T = Q^T H Q (LAPACK's convention: reflector k = I - tau_k v_k v_k^T acts on
+//     rows k+1.., v_k[k+1] = 1, T[k+1][k] = ||H[k+1:, k]||), by one wave: lane l owns
+//     column l of the trailing block, kept whole (both triangles) in LDS, so every
+//     access is a row read or write across the lanes.
+//  2. Every eigenvalue of T by multisection: lane j of each of the 8 waves evaluates
+//     the Sturm count (the number of eigenvalues below x, from the pivots of
+//     T - x I) at one of 8 interior points of the j-th smallest eigenvalue's bracket,
+//     so each pass shrinks every bracket 9x (EH_PASSES passes from the Gershgorin
+//     interval).
+//  3. The top nv = min(kw, r) eigenpairs -- every value the gate compares at the
+//     default thresholds -- by inverse iteration on T (partial-pivoting elimination of
+//     T - sigma I, one lane per eigenpair, start vectors fixed per index, Rayleigh-
+//     quotient shifts), vectors whose eigenvalues lie within 1e-3 ||T|| of the previous
+//     one re-orthogonalised in order after every step; further deflated directions
+//     the gate asks for (thresholds set apart) the same way afterwards.  Then each
+//     vector is back-transformed, Q y.
+//  4. The gate, the deflate / restore weights and d exactly as eig_gate computes them.
+// Degenerate matrices (flagged by the Cholesky) skip 1-3 and come out declined, as
+// in eig_gate.
+// ---------------------------------------------------------------------------
+constexpr int EH_THREADS = 512;
+constexpr int EH_WAVES = EH_THREADS / 64;
+constexpr int EH_ITERS = 3;     // inverse-iteration steps per eigenpair, at most
+constexpr int EH_VL = 32;       // eigenpairs per inverse-iteration batch (lanes)
+constexpr int ZP = RP + 2;      // row pitch (doubles) of the eigenvector rows
+
+union EhScratch {
+  struct {
+    double H[RP * JP];                                 // H, reduced in place
+    double pw[EH_WAVES][RP];                           // the waves' partial products
+  } red;                                               // (step 1)
+  struct {
+    double u0[RP][EH_VL], u1[RP][EH_VL], u2[RP][EH_VL];   // band U of T - sigma I, per lane
+    double y[RP][EH_VL];                                  // the lane's vector
+  } lu;                                                // (step 4)
+  double G[RP * JP];                                   // Q^T Q (step 5)
+};
+
+// Wave-wide reductions of a double: within each row of 16 lanes by DPP moves (lanes
+// l ^ 1, l ^ 2, then the mirrored half-row and row), then the four row results read
+// from lanes 0, 16, 32, 48 -- every lane gets the same value.  All 64 lanes active.
+__device__ __forceinline__ double dpp_d(double v, int ctrl_sel) {
+  const long long bits = __double_as_longlong(v);
+  int lo = (int)(bits & 0xffffffffLL), hi = (int)(bits >> 32);
+  switch (ctrl_sel) {
+    case 0: lo = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, false);
+            hi = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, false); break;   // quad [1,0,3,2]
+    case 1: lo = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xF, 0xF, false);
+            hi = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xF, 0xF, false); break;   // quad [2,3,0,1]
+    case 2: lo = __builtin_amdgcn_mov_dpp(lo, 0x141, 0xF, 0xF, false);
+            hi = __builtin_amdgcn_mov_dpp(hi, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+    default: lo = __builtin_amdgcn_mov_dpp(lo, 0x140, 0xF, 0xF, false);
+             hi = __builtin_amdgcn_mov_dpp(hi, 0x140, 0xF, 0xF, false); break; // row_mirror
+  }
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v += dpp_d(v, 0);
+  v += dpp_d(v, 1);
+  v += dpp_d(v, 2);
+  v += dpp_d(v, 3);
+  return (lane_val(v, 0) + lane_val(v, 16)) + (lane_val(v, 32) + lane_val(v, 48));
+}
+__device__ __forceinline__ double wave_min_d(double v) {
+  v = fmin(v, dpp_d(v, 0));
+  v = fmin(v, dpp_d(v, 1));
+  v = fmin(v, dpp_d(v, 2));
+  v = fmin(v, dpp_d(v, 3));
+  return fmin(fmin(lane_val(v, 0), lane_val(v, 16)), fmin(lane_val(v, 32), lane_val(v, 48)));
+}
+__device__ __forceinline__ double wave_max_d(double v) {
+  v = fmax(v, dpp_d(v, 0));
+  v = fmax(v, dpp_d(v, 1));
+  v = fmax(v, dpp_d(v, 2));
+  v = fmax(v, dpp_d(v, 3));
+  return fmax(fmax(lane_val(v, 0), lane_val(v, 16)), fmax(lane_val(v, 32), lane_val(v, 48)));
+}
+// 1/x from the hardware estimate and one Newton step
+__device__ __forceinline__ double rcp_nr1(double x) {
+  double y = __builtin_amdgcn_rcp(x);
+  return fma(y, fma(-x, y, 1.0), y);
+}
+// the compiler keeps LDS accesses on either side in order; a wave's LDS accesses
+// complete in order, so reads after it see every lane's earlier writes
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Start vector of inverse iteration for eigenpair t: fixed pseudo-random entries in
+// (-1, 1) (a hash of (t, i)), zero past r.
+__device__ __forceinline__ double eh_start(int t, int i, int r) {
+  if (i >= r) return 0.0;
+  unsigned h = (unsigned)(t * RP + i) * 2654435761u;
+  h ^= h >> 15; h *= 2246822519u; h ^= h >> 13;
+  return ((double)(h >> 8) + 0.5) * (2.0 / 16777216.0) - 1.0;
+}
+
+// Inverse iteration for eigenpairs t0 .. t1-1 (t1 - t0 <= EH_VL) on wave 0: lane
+// t - t0 refines lamd[t] (a bracket midpoint on entry, the Rayleigh quotient on exit)
+// and leaves the eigenvector y_t of T in row t of Z (eh_back_transform makes it
+// Q y_t).  Each lane's vector and band factors live in LDS columns (sc.lu.y[i][lane],
+// ...), walked by plain loops.
+__device__ __forceinline__ void eh_inverse_iteration(int t0, int t1, int r, double tn,
+                                                     const double* dd, const double* ee,
+                                                     const double* taus, const double* Vr,
+                                                     double* lamd, double* Z, EhScratch& sc,
+                                                     int l) {
+  const int t = t0 + l;
+  const bool lane = l < EH_VL;            // lanes that own a column of the scratch
+  const bool act = lane && t < t1;
+  const int cl = lane ? l : 0;
+  const double eps_tn = 2.220446049250313e-16 * (tn > 0.0 ? tn : 1.0);
+  double sigma = act ? lamd[t] : 0.0;
+  if (lane) {
+    double n0 = 0.0;
+    for (int i = 0; i < RP; ++i) {
+      const double v = act ? eh_start(t, i, r) : 0.0;
+      n0 = fma(v, v, n0);
+      sc.lu.y[i][cl] = v;
+    }
+    const double s0n = n0 > 0.0 ? rsqrt_nr(n0) : 0.0;
+    for (int i = 0; i < RP; ++i) sc.lu.y[i][cl] *= s0n;
+  }
+  // a step has converged when the solve amplified the unit start vector by 1e8 / ||T||
+  // (the shift then lies within ~1e-8 ||T|| |c| of the eigenvalue, c the start vector's
+  // component along it); at most EH_ITERS steps
+  bool conv = !act;
+  for (int it = 0; it < EH_ITERS; ++it) {
+    if (lane && !conv) {
+      // (T - sigma I) x = y: forward elimination with row interchanges
+      double cur0 = dd[0] - sigma, cur1 = ee[0];
+      double yc = sc.lu.y[0][cl];
+#pragma unroll 4
+      for (int i = 0; i + 1 < RP; ++i) {
+        const double sub = ee[i], nd = dd[i + 1] - sigma, ns = (i + 2 < RP) ? ee[i + 1] : 0.0;
+        const double yn = sc.lu.y[i + 1][cl];
+        const bool sw = fabs(cur0) < fabs(sub);
+        const double piv = sw ? sub : (cur0 != 0.0 ? cur0 : eps_tn);
+        const double mlt = (sw ? cur0 : sub) * rcp_nr(piv);
+        sc.lu.u0[i][cl] = piv;
+        sc.lu.u1[i][cl] = sw ? nd : cur1;
+        sc.lu.u2[i][cl] = sw ? ns : 0.0;
+        sc.lu.y[i][cl] = sw ? yn : yc;
+        yc = sw ? fma(-mlt, yn, yc) : fma(-mlt, yc, yn);
+        const double c0 = sw ? fma(-mlt, nd, cur1) : fma(-mlt, cur1, nd);
+        cur1 = sw ? -mlt * ns : ns;
+        cur0 = c0;
+      }
+      sc.lu.u0[RP - 1][cl] = cur0 != 0.0 ? cur0 : eps_tn;
+      // back substitution, then |x| and the Rayleigh quotient
+      double x1 = 0.0, x2 = 0.0, nrm = 0.0;
+#pragma unroll 4
+      for (int i = RP - 1; i >= 0; --i) {
+        const double yi = i == RP - 1 ? yc : sc.lu.y[i][cl];
+        double s = fma(-sc.lu.u1[i][cl], x1, yi);
+        s = fma(-sc.lu.u2[i][cl], x2, s);
+        const double x = s * rcp_nr(sc.lu.u0[i][cl]);
+        sc.lu.y[i][cl] = x;
+        nrm = fma(x, x, nrm);
+        x2 = x1;
+        x1 = x;
+      }
+      const double inv = act && nrm > 0.0 ? rsqrt_nr(nrm) : 0.0;
+      conv = nrm * tn * tn >= 1e16;
+      double rq = 0.0, rq2 = 0.0, yp = 0.0;
+#pragma unroll 8
+      for (int i = 0; i < RP; ++i) {
+        const double yi = sc.lu.y[i][cl] * inv;
+        sc.lu.y[i][cl] = yi;
+        rq = fma(dd[i] * yi, yi, rq);
+        if (i > 0) rq2 = fma(ee[i - 1] * yp, yi, rq2);
+        yp = yi;
+      }
+      if (act) sigma = fma(2.0, rq2, rq);
+    }
+    const bool done = __all(conv);
+    // eigenvalues within 1e-3 ||T|| of their predecessor: Gram-Schmidt in order
+    const double sprev = __shfl_up(sigma, 1);
+    const bool clus = act && t > t0 && fabs(sigma - sprev) <= 1e-3 * tn;
+    if (__any(clus)) {
+      wave_lds_order();
+      const unsigned long long cmask = __ballot(clus);
+      for (int u = t0 + 1; u < t1; ++u) {
+        if (!((cmask >> (u - t0)) & 1ull)) continue;
+        int s0 = u - 1;
+        while (s0 > t0 && ((cmask >> (s0 - t0)) & 1ull)) --s0;   // first member of u's cluster
+        // lane l: entry l of the vectors (columns u - t0 and q - t0 of the scratch)
+        double zu = sc.lu.y[l][u - t0];
+        for (int q = s0; q < u; ++q) {
+          const double zq = sc.lu.y[l][q - t0];
+          const double dot = wave_sum_d(zq * zu);
+          zu = fma(-dot, zq, zu);
+        }
+        const double nn = wave_sum_d(zu * zu);
+        zu *= nn > 0.0 ? rsqrt_nr(nn) : 0.0;
+        sc.lu.y[l][u - t0] = zu;
+        wave_lds_order();
+      }
+    }
+    wave_lds_order();
+    if (done) break;
+  }
+  // the eigenvalue of the final vector (a cluster's Gram-Schmidt may have moved it)
+  if (act) {
+    double rq = 0.0, rq2 = 0.0, yp = 0.0;
+#pragma unroll 8
+    for (int i = 0; i < RP; ++i) {
+      const double yi = sc.lu.y[i][cl];
+      rq = fma(dd[i] * yi, yi, rq);
+      if (i > 0) rq2 = fma(ee[i - 1] * yp, yi, rq2);
+      yp = yi;
+    }
+    sigma = fma(2.0, rq2, rq);
+  }
+  if (act) {
+    lamd[t] = sigma;
+    for (int i = 0; i < RP; ++i) Z[t * ZP + i] = sc.lu.y[i][cl];   // before the back-transform
+  }
+  wave_lds_order();
+}
+
+// Z[t] <- Q Z[t] = H_0 H_1 ... H_{r-3} Z[t] for t < nvec, the last reflector first:
+// wave w takes vectors w, w + 8, ... (up to 4 at once, for independent reduction
+// chains), lane i row i; each reflector costs one DPP reduction per vector.
+__device__ __forceinline__ void eh_back_transform(int nvec, int r, const double* taus,
+                                                  const double* Vr, double* Z, int wave, int l) {
+  for (int t0 = wave; t0 < nvec; t0 += 4 * EH_WAVES) {
+    double z[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t = t0 + q * EH_WAVES;
+      z[q] = t < nvec ? Z[t * ZP + l] : 0.0;
+    }
+    for (int k = r - 3; k >= 0; --k) {
+      const double tk = taus[k];
+      if (tk == 0.0) continue;
+      const double vi = Vr[k * RP + l];   // zero for rows <= k and past r
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const double sq = wave_sum_d(vi * z[q]) * tk;
+        z[q] = fma(-sq, vi, z[q]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t = t0 + q * EH_WAVES;
+      if (t < nvec) Z[t * ZP + l] = z[q];
+    }
+  }
+}
+
+__global__ __launch_bounds__(EH_THREADS) void eig_head_gate(
+    const double* __restrict__ part, GateParams gp, const int* __restrict__ degen,
+    float* __restrict__ s_out, int s_ld, float* __restrict__ Ub, float* __restrict__ UbS,
+    long long* __restrict__ k_out, int* __restrict__ k_int, float* __restrict__ cw,
+    float* __restrict__ cr, const double* __restrict__ qpart, const double* __restrict__ asq,
+    int asq_n, float* __restrict__ d_out, int* __restrict__ wflag) {
+  __shared__ __attribute__((aligned(16))) EhScratch sc;
+  __shared__ __attribute__((aligned(16))) double Vr[RP * RP];   // reflector k in row k
+  __shared__ __attribute__((aligned(16))) double Z[RP * ZP];    // eigenvector t in row t
+  __shared__ double dd[RP], ee[RP], e2s[RP], taus[RP], lamd[RP];
+  __shared__ int cnt[2][EH_THREADS];
+  __shared__ float sv[RP];
+  __shared__ double s_lo, s_hi, s_tn;
+  const int b = blockIdx.x, tid = threadIdx.x, l = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = gp.r;
+  const bool bad = degen && degen[b];
+  {
+    const double* pb = part + (long long)b * GRAM_CHUNKS * RP * RP;
+    for (int e = tid; e < RP * RP; e += EH_THREADS) {
+      const int i = e / RP, j = e % RP;
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < GRAM_CHUNKS; ++c) acc += pb[(long long)c * RP * RP + e];
+      sc.red.H[i * JP + j] = (i < r && j < r) ? acc : 0.0;
+    }
+  }
+  __syncthreads();
+  // ---- 1. tridiagonal reduction: every wave forms each reflector itself (the same
+  // values: same inputs, same order), so that only the matrix-vector product and the
+  // rank-2 update, whose rows (every 8th) the waves share, need workgroup barriers
+  if (!bad) {
+    double* H = sc.red.H;
+    for (int k = 0; k + 2 < r; ++k) {
+      const double xi = (l > k && l < r) ? H[k * JP + l] : 0.0;   // H[l][k] = H[k][l]
+      const double x0 = lane_val(xi, k + 1);
+      const double sg = wave_sum_d(l > k + 1 ? xi * xi : 0.0);
+      double vl = 0.0, tk = 0.0, ek = x0;   // sg == 0: already reduced, no reflection
+      if (sg != 0.0) {
+        const double mu = sqrt(x0 * x0 + sg);
+        const double v0 = x0 <= 0.0 ? x0 - mu : -sg / (x0 + mu);
+        const double v02 = v0 * v0;
+        tk = 2.0 * v02 / (sg + v02);
+        const double iv0 = 1.0 / v0;
+        vl = l == k + 1 ? 1.0 : ((l > k + 1 && l < r) ? xi * iv0 : 0.0);
+        ek = mu;
+      }
+      if (wave == 0) {
+        Vr[k * RP + l] = vl;
+        if (l == 0) { dd[k] = H[k * JP + k]; ee[k] = ek; taus[k] = tk; }
+      }
+      if (tk != 0.0) {   // uniform over the workgroup
+        // p = tau H22 v: wave w sums rows k+1+w, k+1+w+8, ... (lane l: column l)
+        double a0 = 0.0, a1 = 0.0;
+        int j = k + 1 + wave;
+        for (; j + EH_WAVES < r; j += 2 * EH_WAVES) {
+          a0 = fma(H[j * JP + l], lane_val(vl, j), a0);
+          a1 = fma(H[(j + EH_WAVES) * JP + l], lane_val(vl, j + EH_WAVES), a1);
+        }
+        if (j < r) a0 = fma(H[j * JP + l], lane_val(vl, j), a0);
+        sc.red.pw[wave][l] = a0 + a1;
+        __syncthreads();
+        double pl = 0.0;
+#pragma unroll
+        for (int w = 0; w < EH_WAVES; ++w) pl += sc.red.pw[w][l];   // same order in every wave
+        pl = (l > k && l < r) ? tk * pl : 0.0;
+        const double K = wave_sum_d(pl * vl);
+        const double wl = pl - (0.5 * tk * K) * vl;
+        // H22 -= v w^T + w v^T, rows k+1+w, k+1+w+8, ... by wave w
+        for (int jj = k + 1 + wave; jj < r; jj += EH_WAVES) {
+          const double vj = lane_val(vl, jj), wj = lane_val(wl, jj);
+          if (l > k && l < r) {
+            double h = H[jj * JP + l];
+            h = fma(-vj, wl, h);
+            h = fma(-wj, vl, h);
+            H[jj * JP + l] = h;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (wave == 0) {
+      // the trailing 2 x 2 (or 1 x 1) block; padding past r: a diagonal far above the
+      // spectrum, decoupled (zero off-diagonal), so it never counts and never mixes in
+      if (l == 0) {
+        if (r >= 2) {
+          dd[r - 2] = H[(r - 2) * JP + r - 2];
+          dd[r - 1] = H[(r - 1) * JP + r - 1];
+          ee[r - 2] = H[(r - 1) * JP + r - 2];
+          taus[r - 2] = 0.0;
+        } else {
+          dd[0] = H[0];
+        }
+      }
+      wave_lds_order();
+      double gl = INFINITY, gh = -INFINITY;
+      if (l < r) {
+        const double em = l > 0 ? fabs(ee[l - 1]) : 0.0, ep = l + 1 < r ? fabs(ee[l]) : 0.0;
+        gl = dd[l] - em - ep;
+        gh = dd[l] + em + ep;
+      }
+      const double lo = wave_min_d(gl), hi = wave_max_d(gh);
+      const double tn = fmax(fabs(lo), fabs(hi));
+      if (l >= r) dd[l] = 2.0 * tn + 1.0;
+      if (l + 1 >= r) ee[l] = 0.0;
+      if (l + 2 >= r && l < r) taus[l] = 0.0;
+      wave_lds_order();
+      e2s[l] = ee[l] * ee[l];
+      if (l == 0) {   // brackets widened by rounding-level margins
+        const double mg = 4.0 * 2.220446049250313e-16 * (tn * RP) + 1e-300;
+        s_lo = lo - mg;
+        s_hi = hi + mg;
+        s_tn = tn;
+      }
+    }
+  }
+  __syncthreads();
+  // ---- 2. the top nE = min(kw, r) eigenvalues (every value the gate compares) by
+  // multisection: nE <= 32: 16 threads per eigenvalue, each evaluating the Sturm count
+  // at one of 16 interior points of its bracket (17 sub-intervals per pass); nE > 32:
+  // 8 threads (9 sub-intervals)
+  const int nE = min(gp.kw, r);
+  const int npt = nE <= 32 ? 16 : 8;           // points per bracket
+  const int slot = tid / npt, pt = tid % npt;  // eigenvalue slot (descending), point
+  if (!bad) {
+    double e2max = 0.0;
+    for (int i = 0; i + 1 < r; ++i) e2max = fmax(e2max, e2s[i]);
+    const double pivmin = 2.2250738585072014e-308 * fmax(1.0, e2max);
+    const int npass = npt == 16 ? 9 : 12;      // brackets ~2 ||T|| / 17^9 or / 9^12
+    const double inv_sect = 1.0 / (double)(npt + 1);
+    double L = s_lo, U = s_hi;
+    const int j = r - 1 - slot;                // ascending index of the eigenvalue
+    const bool live = slot < nE;
+    for (int p = 0; p < npass; ++p) {
+      // (the same expression as the readers' below, so all threads agree on the points)
+      const double x = fma(U - L, (double)(pt + 1) * inv_sect, L);
+      int c = 0;
+      if (live) {
+        asm volatile("" ::: "memory");   // T's rows are read in batches, not all up front
+        double q = dd[0] - x;
+        if (fabs(q) < pivmin) q = -pivmin;
+        c = q < 0.0;
+#pragma unroll
+        for (int i = 1; i < RP; ++i) {
+          if ((i & 7) == 0) asm volatile("" ::: "memory");
+          q = (dd[i] - x) - e2s[i - 1] * rcp_nr1(q);
+          if (fabs(q) < pivmin) q = -pivmin;
+          c += q < 0.0;
+        }
+      }
+      cnt[p & 1][tid] = c;
+      __syncthreads();
+      double nL = L, nU = U;
+      bool found = false;
+      for (int w = 0; w < npt; ++w) {
+        const double xw = fma(U - L, (double)(w + 1) * inv_sect, L);
+        if (!found) {
+          if (cnt[p & 1][slot * npt + w] > j) { nU = xw; found = true; }
+          else nL = xw;
+        }
+      }
+      L = nL;
+      U = nU;
+    }
+    if (pt == 0 && live) lamd[slot] = 0.5 * (L + U);   // descending
+  }
+  __syncthreads();
+  // ---- 3. gate, fp32 comparisons as torch does them (deflation_batched.py:177-180),
+  // on the bracket midpoints (brackets ~1e-11 ||T||: every comparison is decided unless
+  // a value lies within ~1e-8 relative of its threshold)
+  if (tid < RP) {
+    float sval = 0.f;
+    if (tid < nE && !bad) {
+      const double ev = lamd[tid];
+      sval = (float)sqrt(ev > 0.0 ? ev : 0.0);
+    }
+    sv[tid] = sval;
+  }
+  __syncthreads();
+  const float s0 = sv[0];
+  const float thr = gp.thresh * s0;
+  int kr = 0;
+  for (int j = 0; j < nE; ++j) kr += sv[j] > thr;
+  // (thresh >= ratio: whenever the gate fires, every value past the top nE lies below
+  // sv[kw-1] < ratio s0 <= thr, so the top nE hold the whole count)
+  const bool could_fire = (sv[gp.kw - 1] < gp.ratio * s0) && kr >= 1;
+  const bool fired = could_fire && kr < r;
+  const int kk = kr < 1 ? 1 : (kr > r - 1 ? r - 1 : kr);
+  // ---- 4. the deflated eigenpairs (wave 0): inverse iteration, Rayleigh-quotient
+  // eigenvalues, back-transform; their singular values replace the bracket values
+  if (fired) {
+    if (!bad && wave == 0)
+      for (int t0 = 0; t0 < kk; t0 += EH_VL)
+        eh_inverse_iteration(t0, min(t0 + EH_VL, kk), r, s_tn, dd, ee, taus, Vr, lamd, Z, sc, l);
+    __syncthreads();
+    if (!bad) eh_back_transform(kk, r, taus, Vr, Z, wave, l);
+    __syncthreads();
+    if (tid < kk) {
+      const double ev = lamd[tid];
+      sv[tid] = (float)sqrt(ev > 0.0 ? ev : 0.0);
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    k_out[b] = fired ? (long long)kk : 0LL;
+    k_int[b] = fired ? kk : 0;
+  }
+  const int nh = fired ? kk : 0;   // columns of Ub filled
+  if (tid < RP) {
+    if (tid < r) s_out[(long long)b * s_ld + tid] = sv[tid];
+    const float h = (fired && tid < kk) ? 1.f : 0.f;
+    cw[(long long)b * RP + tid] = sv[tid] * h;
+    cr[(long long)b * RP + tid] = h * (1.0f / gp.pad);
+  }
+  float* Ubb = Ub + (long long)b * RP * RP;
+  float* UbSb = UbS + (long long)b * RP * RP;
+  for (int e = tid; e < RP * RP; e += EH_THREADS) {
+    const int a = e / RP, t = e % RP;   // row a of Ub, column t
+    float u = 0.f;
+    if (a < r && t < nh && !bad) u = (float)Z[t * ZP + a];
+    Ubb[e] = u;
+    UbSb[e] = sv[t] > 0.f ? u / sv[t] : 0.f;
+  }
+  if (d_out && fired) {   // Q^T Q, summed by every thread
+    const double* qb = qpart + (long long)b * GRAM_CHUNKS * RP * RP;
+    for (int e = tid; e < RP * RP; e += EH_THREADS) {
+      const int i = e / RP, j = e % RP;
+      double acc = 0.0;
+#pragma unroll
+      for (int c = 0; c < GRAM_CHUNKS; ++c) acc += qb[(long long)c * RP * RP + e];
+      sc.G[i * JP + j] = (i < r && j < r) ? acc : 0.0;
+    }
+    __syncthreads();
+  }
+  if (!d_out || wave != 0) return;
+  // ||W||_F^2 = ||A||^2 - sum_{t<k} lambda_t (2 - G_t), G_t = Ub_t^T (Q^T Q) Ub_t (see
+  // eig_gate)
+  double asum = 0.0;
+  for (int i = l; i < asq_n; i += 64) asum += asq[(long long)b * asq_n + i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) asum += __shfl_xor(asum, o);
+  double w2 = asum;
+  if (fired) {
+    const double* G = sc.G;
+    double head = 0.0;
+    for (int t = 0; t < kk; ++t) {
+      double y = 0.0;   // (Q^T Q Ub_t)_l, with Ub_t rounded to fp32 as stored
+      if (l < r)
+        for (int c = 0; c < r; ++c) y = fma(G[l * JP + c], (double)(float)Z[t * ZP + c], y);
+      double gt = (l < r) ? (double)(float)Z[t * ZP + l] * y : 0.0;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) gt += __shfl_xor(gt, o);
+      head += lamd[t] * (2.0 - gt);
+    }
+    w2 = asum - head;
+  }
+  if (l == 0) d_out[b] = (float)sqrt(w2 > 0.0 ? w2 : 0.0) + 1e-7f;
+  if (l == 0 && wflag) wflag[b] = fired && w2 < 1e-2 * asum ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
 // Restore pass (deflation_batched.py:184-188):
 //   X0 = (A - U diag(s h) V^T) / d + U diag(h / pad) V^T
 //      = A / d - sum_{t<k} U[i][t] (cw_t / d - cr_t) V[j][t]
@@ -1721,11 +2241,20 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
   // H = Bp Bp^T = Gram of Bp^T
   if ((rc = gram(st, w.Bt, B, m, w.gram))) return rc;
   if (d && (rc = gram(st, w.Q, B, n, w.gramq))) return rc;
-  hipLaunchKernelGGL(eig_gate, dim3(B), dim3(EG_THREADS), 0, st, w.gram, gp, w.degen, w.s, RP, w.Ub,
-                     w.UbS, k_out, w.kint, w.cw, w.cr, d ? w.gramq : nullptr,
-                     d ? w.asq : nullptr, ceil_div(n, fast ? SKR_ROWS : SG_ROWS), d,
-                     d ? w.wflag : nullptr);
-  DMH_CHECK_LAUNCH("eig_gate");
+  if (d && gp.thresh >= gp.ratio) {
+    // clip / fused paths: the head eigenpairs only (with the clip threshold at or above
+    // the gate ratio, every deflated direction lies within the gate window)
+    hipLaunchKernelGGL(eig_head_gate, dim3(B), dim3(EH_THREADS), 0, st, w.gram, gp, w.degen, w.s,
+                       RP, w.Ub, w.UbS, k_out, w.kint, w.cw, w.cr, w.gramq, w.asq,
+                       ceil_div(n, fast ? SKR_ROWS : SG_ROWS), d, w.wflag);
+    DMH_CHECK_LAUNCH("eig_head_gate");
+  } else {
+    hipLaunchKernelGGL(eig_gate, dim3(B), dim3(EG_THREADS), 0, st, w.gram, gp, w.degen, w.s, RP,
+                       w.Ub, w.UbS, k_out, w.kint, w.cw, w.cr, d ? w.gramq : nullptr,
+                       d ? w.asq : nullptr, ceil_div(n, fast ? SKR_ROWS : SG_ROWS), d,
+                       d ? w.wflag : nullptr);
+    DMH_CHECK_LAUNCH("eig_gate");
+  }
   // U = Q Ub ; V = Bp^T Ub diag(1/s)
   return launch_uv(st, w, B, n, m);
 }

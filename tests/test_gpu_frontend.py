@@ -297,3 +297,58 @@ def test_head_dominated_divisor(N, bulk):
     assert bool(torch.isfinite(X0).all())
     # the deflated entry: 1/pad on the head, the bulk at unit Frobenius norm
     assert rel(X0, X0o) < 1e-3
+
+
+def _clip_vs_fp64(N, A, kw, ratio, thresh, name):
+    """rmfro_clip on the GPU, the oracle in fp32 (the reference arithmetic) and the same
+    algorithm in fp64; returns (k, k_oracle, k_fp64) and checks that the library's d and
+    X0 are at least as close to the fp64 result as the oracle's fp32 ones."""
+    B, n, m = A.shape
+    r, _ = O.sketch_dims(m)
+    Om = O.draw_omega(B, m, r, seed=m + B)
+    X0, k, d = N.rmfro_clip(A.to(DEV), Om.to(DEV), kw, ratio, thresh, O.DIVISOR_PAD,
+                            out_dtype=torch.float32)
+    X0o, ko, do = O.rmfro_clip(A, Om, ratio=ratio, thresh=thresh)
+    X08, k8, d8 = O.rmfro_clip(A.double(), Om.double(), ratio=ratio, thresh=thresh)
+    e_lib, e_ref = rel(X0.cpu().double(), X08), rel(X0o.double(), X08)
+    dd_lib = float(((d.cpu().double() - d8).abs() / d8).max())
+    dd_ref = float(((do.double() - d8).abs() / d8).max())
+    log_parity("frontend", name, x0_vs_fp64=e_lib, oracle_x0_vs_fp64=e_ref, d_vs_fp64=dd_lib,
+               oracle_d_vs_fp64=dd_ref)
+    assert e_lib <= 2 * e_ref + 1e-6, (e_lib, e_ref)
+    assert dd_lib <= 2 * dd_ref + 1e-6, (dd_lib, dd_ref)
+    return k.cpu().tolist(), ko.tolist(), k8.tolist()
+
+
+@pytest.mark.parametrize("case", ["repeated_head", "wide_head", "two_column_sketch"])
+def test_clip_head_eigenpairs(N, case):
+    """The clip's gate eigen-solve (tridiagonal reduction, multisection for the top kw
+    eigenvalues, inverse iteration on the deflated head): four equal head singular
+    values (an eigenvalue cluster, re-orthogonalised), a 30-direction head in the
+    widest gate window (kw = 32), and a 2-column sketch (r = 2, kw = 1: the gate cannot
+    fire).  Gate decisions identical to the oracle's in fp32 and fp64."""
+    from defmuon_amd import synthetic as S
+    if case == "repeated_head":
+        A = S.spiked_batch(3, 2048, 512, seed=21, n_spikes=4, hi=30.0, lo=30.0)
+        want = [4, 4, 4]
+    elif case == "wide_head":
+        A = S.spiked_batch(2, 2560, 1280, seed=22, n_spikes=30, hi=60.0, lo=12.0)
+        want = [30, 30]
+    else:
+        A = S.spiked_batch(3, 300, 40, seed=23, n_spikes=1, hi=20.0, lo=20.0)
+        want = [0, 0, 0]
+    _, kw = O.sketch_dims(A.shape[-1])
+    k, ko, k8 = _clip_vs_fp64(N, A, kw, O.GATE_RATIO, O.DEFLATE_THRESH, f"clip head {case}")
+    assert k == ko == k8 == want
+
+
+def test_clip_threshold_below_ratio(N):
+    """A clip threshold below the gate ratio (DEFMUON_DEFL_THRESH < DEFMUON_DEFL_RATIO)
+    deflates past the gate window (16 directions, kw = 13): the library takes its
+    full Jacobi eigen-solve there; k, d and X0 as the oracle's at those thresholds."""
+    from defmuon_amd import synthetic as S
+    A = S.spiked_batch(3, 2048, 512, seed=24, n_spikes=16, hi=100.0, lo=5.0)
+    _, kw = O.sketch_dims(512)
+    assert kw == 13
+    k, ko, k8 = _clip_vs_fp64(N, A, kw, 0.10, 0.04, "clip thresh 0.04 < ratio 0.10")
+    assert k == ko == k8 == [16, 16, 16]
