@@ -11,7 +11,8 @@
 //   skinny_gemm<ROWS>   C = A X       (n x RP)   fp32 MFMA 32x32x2, A streamed by rows
 //   skinny_gemm<COLS>   C = A^T Y     (m x RP)   fp32 MFMA 32x32x2, A streamed by columns
 //   gram_partials       partial fp64 Gram Y^T Y over row chunks
-//   chol_inv            sum partials, Cholesky in LDS (fp64), M = L^-T  (one workgroup)
+//   chol_inv            sum partials, Cholesky in LDS (fp64, columns over 8 waves),
+//                       M = L^-T  (one workgroup)
 //   right_mult          C = Y M       (rows x RP) x (RP x RP)
 //   eig_gate            Jacobi eigen-decomposition of Bp Bp^T in LDS (fp64) -> s, Ub;
 //                       the deflation gate and the per-column deflate/restore weights
@@ -183,7 +184,22 @@ __device__ __forceinline__ double lane_val(double v, int lane) {
 // of the diagonal of a lane's row are updated too (their values are never read), which
 // keeps the update free of per-lane predication.  Then L goes to LDS by rows and lane
 // l computes column l of L^-1 by forward substitution.
-constexpr int CHOL_THREADS = 256;   // all sum the Gram partials; wave 0 factors
+// 1/sqrt(x) and 1/x in fp64 from the hardware estimates plus Newton steps
+// (relative error ~1e-16 for the positive normal arguments used here)
+__device__ __forceinline__ double rsqrt_nr(double x) {
+  double y = __builtin_amdgcn_rsq(x);
+  y = y * (1.5 - 0.5 * x * y * y);
+  y = y * (1.5 - 0.5 * x * y * y);
+  return y;
+}
+__device__ __forceinline__ double rcp_nr(double x) {
+  double y = __builtin_amdgcn_rcp(x);
+  y = y * (2.0 - x * y);
+  y = y * (2.0 - x * y);
+  return y;
+}
+
+constexpr int CHOL_THREADS = 512;   // all sum the Gram partials and factor; wave 0 inverts
 
 __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restrict__ part, int r,
                                                          float* __restrict__ M,
@@ -193,6 +209,7 @@ __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restric
   const int b = blockIdx.x, tid = threadIdx.x, l = tid & 63;
   __shared__ __attribute__((aligned(16))) double Ls[RP * LP];   // Gram, then L by rows
   __shared__ __attribute__((aligned(16))) double Lc[RP * RP];   // row k: column k of L
+  __shared__ double Ld[RP];                                     // 1 / L[k][k]
   {
     // every load of the partials issued up front (summed in chunk order)
     const double* pb = part + (long long)b * GRAM_CHUNKS * RP * RP;
@@ -211,42 +228,53 @@ __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restric
     }
   }
   __syncthreads();
-  if (tid >= 64) return;
-  double g[RP];
+  // right-looking Cholesky with the columns split over the 8 waves: lane l holds row l,
+  // wave w columns CW w .. CW w + CW - 1 (g[c] = G[l][CW w + c]).  Step k: the owner of
+  // column k forms L[.][k] (one reciprocal square root of the pivot) and publishes it
+  // in row k of Lc; after one barrier every wave updates its columns past k.  Every
+  // element sees the same operations in the same order as in a one-wave loop.
+  constexpr int CW = RP / (CHOL_THREADS / 64);   // columns per wave
+  static_assert(RP % (CHOL_THREADS / 64) == 0, "the waves share the columns evenly");
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  double g[CW];
 #pragma unroll
-  for (int j = 0; j < RP; ++j) g[j] = Ls[l * LP + j];
-  // right-looking Cholesky: after step k, g[k] of lane l >= k holds L[l][k]
+  for (int c = 0; c < CW; ++c) g[c] = Ls[l * LP + CW * wave + c];
   bool fail = false;
 #pragma unroll
   for (int k = 0; k < RP; ++k) {
-    const double dk = lane_val(g[k], k);
-    fail |= !(dk > 0.0) || !isfinite(dk);
-    const double lkk = sqrt(dk > 0.0 ? dk : 1.0);
-    const double lik = (l > k) ? g[k] / lkk : (l == k ? lkk : 0.0);
-    g[k] = lik;
-    if (k + 1 < RP) {
+    const int kc = k % CW;
+    if (wave == k / CW) {
+      const double dk = lane_val(g[kc], k);
+      fail |= !(dk > 0.0) || !isfinite(dk);
+      const double dkp = dk > 0.0 ? dk : 1.0;
+      const double rs = rsqrt_nr(dkp);
+      const double lik = (l > k) ? g[kc] * rs : (l == k ? dkp * rs : 0.0);
+      g[kc] = lik;
       Lc[k * RP + l] = lik;
-      // a wave's LDS accesses complete in order: the reads below see every lane's write
-      asm volatile("" ::: "memory");
+      if (l == 0) Ld[k] = rs;
+    }
+    __syncthreads();
+    if (k + 1 < RP) {
+      const double lik = Lc[k * RP + l];
 #pragma unroll
-      for (int j = k + 1; j < RP; ++j) {
-        g[j] = fma(-lik, Lc[k * RP + j], g[j]);
-        // keep the update in this step (otherwise the compiler defers it to the
-        // step that needs g[j], holding every loaded column value until then) and
-        // the column loads in batches of 8
-        asm volatile("" : "+v"(g[j]));
-        if ((j & 7) == 7) asm volatile("" ::: "memory");
+      for (int c = 0; c < CW; ++c) {
+        if (CW * wave + c > k) g[c] = fma(-lik, Lc[k * RP + CW * wave + c], g[c]);
       }
     }
   }
-  // L by rows into LDS; x = column l of L^-1 by forward substitution,
+  // L by rows into LDS (each wave its columns); a failed pivot anywhere declines
+  __shared__ int s_fail;
+  if (tid == 0) s_fail = 0;
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < CW; ++c) Ls[l * LP + CW * wave + c] = g[c];
+  if (fail) s_fail = 1;
+  __syncthreads();
+  if (tid >= 64) return;
+  fail = s_fail != 0;
+  // x = column l of L^-1 by forward substitution,
   // L[i][i] x_i = delta_il - sum_{t<i} L[i][t] x_t (broadcast reads of row i of L);
   // x_i = 0 for i < l
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int j = 0; j < RP; ++j) Ls[l * LP + j] = g[j];
-  asm volatile("" ::: "memory");
   double x[RP];
 #pragma unroll
   for (int i = 0; i < RP; ++i) {
@@ -258,7 +286,7 @@ __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restric
       if ((t & 7) == 6) asm volatile("" ::: "memory");   // row loads in batches of 8
     }
     if (i & 1) s0 = fma(-Ls[i * LP + i - 1], x[i - 1], s0);
-    x[i] = (i < l) ? 0.0 : (s0 + s1) / Ls[i * LP + i];
+    x[i] = (i < l) ? 0.0 : (s0 + s1) * Ld[i];
   }
   // M = L^-T: M[a][c] = (L^-1)[c][a], so row l of M is x
   float* Mb = M + (long long)b * RP * RP + (long long)l * RP;
@@ -898,20 +926,6 @@ __device__ __forceinline__ int jac_next(int x) {
   return (x & 1) ? x + 2 : x - 2;
 }
 
-// 1/sqrt(x) and 1/x in fp64 from the hardware estimates plus Newton steps
-// (relative error ~1e-16 for the positive normal arguments used here)
-__device__ __forceinline__ double rsqrt_nr(double x) {
-  double y = __builtin_amdgcn_rsq(x);
-  y = y * (1.5 - 0.5 * x * y * y);
-  y = y * (1.5 - 0.5 * x * y * y);
-  return y;
-}
-__device__ __forceinline__ double rcp_nr(double x) {
-  double y = __builtin_amdgcn_rcp(x);
-  y = y * (2.0 - x * y);
-  y = y * (2.0 - x * y);
-  return y;
-}
 
 __global__ __launch_bounds__(EG_THREADS) void eig_gate(const double* __restrict__ part,
                                                        GateParams gp,
