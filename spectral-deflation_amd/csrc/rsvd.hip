@@ -154,16 +154,6 @@ __global__ __launch_bounds__(256) void skinny_gemm(const float* __restrict__ A, 
 #undef DMH_SG_LOAD
 }
 
-__device__ void sum_gram_partials(const double* part, int b, int r, double (*G)[RP + 1]) {
-  const double* p = part + (long long)b * GRAM_CHUNKS * RP * RP;
-  for (int e = threadIdx.x; e < RP * RP; e += blockDim.x) {
-    const int i = e / RP, j = e % RP;
-    double s = 0.0;
-    for (int c = 0; c < GRAM_CHUNKS; ++c) s += p[(long long)c * RP * RP + e];
-    G[i][j] = (i < r && j < r) ? s : 0.0;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Cholesky of the r x r Gram (lower, in place) and M = L^-T, one workgroup per
 // matrix.  A non-positive or non-finite pivot marks the matrix degenerate: M is
@@ -176,14 +166,6 @@ __device__ __forceinline__ double lane_val(double v, int lane) {
   return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// One wavefront per matrix.  Lane l keeps row l of the (identity-padded) Gram in
-// registers; the factorization and the inversion are fully unrolled over the 64 x 64
-// problem.  Step k of the right-looking Cholesky broadcasts the pivot by readlane and
-// the new column L[k.., k] through LDS (lane i writes L[i][k]; every lane then reads
-// the column with broadcast LDS reads, which keep the values in VGPRs).  Entries right
-// of the diagonal of a lane's row are updated too (their values are never read), which
-// keeps the update free of per-lane predication.  Then L goes to LDS by rows and lane
-// l computes column l of L^-1 by forward substitution.
 // 1/sqrt(x) and 1/x in fp64 from the hardware estimates plus Newton steps
 // (relative error ~1e-16 for the positive normal arguments used here)
 __device__ __forceinline__ double rsqrt_nr(double x) {
@@ -199,6 +181,15 @@ __device__ __forceinline__ double rcp_nr(double x) {
   return y;
 }
 
+// One workgroup per matrix.  Lane l of every wave keeps row l of the (identity-padded)
+// Gram, each wave a block of its columns, in registers; the factorization and the
+// inversion are fully unrolled over the 64 x 64 problem.  Step k of the right-looking
+// Cholesky: the wave owning column k broadcasts the pivot by readlane and publishes the
+// new column L[k.., k] through LDS; every wave then updates its columns with broadcast
+// LDS reads.  Entries right of the diagonal of a lane's row are updated too (their
+// values are never read), which keeps the update free of per-lane predication.  Then
+// L goes to LDS by rows and lane l of wave 0 computes column l of L^-1 by forward
+// substitution.
 constexpr int CHOL_THREADS = 512;   // all sum the Gram partials and factor; wave 0 inverts
 
 __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restrict__ part, int r,
