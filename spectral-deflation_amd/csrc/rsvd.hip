@@ -341,12 +341,14 @@ __device__ __forceinline__ void right_mult_tile(const RightMult& p, int b, int r
       acc[i][3] = fmaf(y, m.w, acc[i][3]);
     }
   }
+  if (C) {   // (null when only the transposed product is read downstream)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = r0 + 4 * ty + i;
-    if (row < rows)
-      *(float4*)&C[(long long)b * c_bs + (long long)row * RP + 4 * tx] =
-          make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    for (int i = 0; i < 4; ++i) {
+      const int row = r0 + 4 * ty + i;
+      if (row < rows)
+        *(float4*)&C[(long long)b * c_bs + (long long)row * RP + 4 * tx] =
+            make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    }
   }
   if (!CT) return;
   float* CTb = CT + (long long)b * RP * ldct;
@@ -2137,8 +2139,10 @@ static int gram(hipStream_t st, const float* Y, int B, int rows, double* part) {
 
 // Q = orth(Y) by CholeskyQR (Y, Q: rows x RP), `passes` times; QT (optional, RP x rows):
 // Q transposed, for the split-bf16 skinny GEMMs.
+// need_q = false (with QT given): Q itself is not read afterwards, only QT -- the last
+// pass writes QT alone
 static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int rows, int r,
-                int passes, const RsvdWs& w, float* QT = nullptr) {
+                int passes, const RsvdWs& w, float* QT = nullptr, bool need_q = true) {
   const float* src = Y;
   int rc;
   for (int p = 0; p < passes; ++p) {
@@ -2147,7 +2151,8 @@ static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int
     if ((rc = gram(st, src, B, rows, w.gram))) return rc;
     hipLaunchKernelGGL(chol_inv, dim3(B), dim3(CHOL_THREADS), 0, st, w.gram, r, w.M, w.degen);
     DMH_CHECK_LAUNCH("chol_inv");
-    const RightMult rm{src, rows, (long long)rows * RP, w.M, dst, (long long)rows * RP,
+    const RightMult rm{src, rows, (long long)rows * RP, w.M,
+                       last && QT && !need_q ? (float*)nullptr : dst, (long long)rows * RP,
                        last ? QT : (float*)nullptr, rows};
     hipLaunchKernelGGL(right_mult, dim3(ceil_div(rows, 64), B), dim3(256), 0, st, rm);
     DMH_CHECK_LAUNCH("right_mult");
@@ -2213,12 +2218,14 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
                        (long long)m * r, w.XT, m);
     DMH_CHECK_LAUNCH("transpose Omega");
     if ((rc = skr(st, A, B, n, m, w.XT, w.Y, d ? w.asq : nullptr))) return rc;
-    if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT))) return rc;
+    // (Q is read only after the last power iteration: the earlier orthonormalisations,
+    // and every one of Z, feed the next skinny product through their transposes alone)
+    if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT, niter == 0))) return rc;
     for (int it = 0; it < niter; ++it) {
       if ((rc = skc(st, A, B, n, m, w.QT, w.Z, w))) return rc;
-      if ((rc = orth(st, w.Z, w.Zq, w.V, B, m, r, passes, w, w.XT))) return rc;
+      if ((rc = orth(st, w.Z, w.Zq, w.V, B, m, r, passes, w, w.XT, false))) return rc;
       if ((rc = skr(st, A, B, n, m, w.XT, w.Y, nullptr))) return rc;
-      if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT))) return rc;
+      if ((rc = orth(st, w.Y, w.Q, w.U, B, n, r, passes, w, w.QT, it == niter - 1))) return rc;
     }
     if ((rc = skc(st, A, B, n, m, w.QT, w.Bt, w))) return rc;
   } else {
