@@ -597,7 +597,11 @@ __device__ __forceinline__ void sk_pin(SkStage& st) {
                    "+v"(st.v[q][h].w));
 }
 
-template <int SPLITS>
+// PERM = false: index k of the chunk at position k of its row.  PERM = true: the
+// order of sk_rows' 16x16 fragments -- within each 32-index step, the 4-index group
+// a = 0..7 at position 8a (a < 4) or 8(a - 4) + 4 (a >= 4), so positions 8g .. 8g + 7
+// hold the indices 4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3.
+template <int SPLITS, bool PERM = false>
 __device__ __forceinline__ void sk_stage_store(const SkStage& st, bf16* buf, int tid) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
@@ -607,8 +611,20 @@ __device__ __forceinline__ void sk_stage_store(const SkStage& st, bf16* buf, int
                         st.v[q][1].x, st.v[q][1].y, st.v[q][1].z, st.v[q][1].w};
     bf16x8 t[SPLITS];
     split_bf16<SPLITS>(x, t);
+    if (PERM) {
+      // the 8 indices are the 4-index groups a0 and a0 + 1 (a0 even) of step kk / 32
+      const int a0 = (kk & 31) >> 2, step = kk & ~31;
+      const int p0 = step + (a0 < 4 ? 8 * a0 : 8 * (a0 - 4) + 4), p1 = p0 + 8;
 #pragma unroll
-    for (int s = 0; s < SPLITS; ++s) *(bf16x8*)(buf + s * SK_TERM + c * SK_PITCH + kk) = t[s];
+      for (int s = 0; s < SPLITS; ++s) {
+        bf16* row = buf + s * SK_TERM + c * SK_PITCH;
+        *(bf16x4*)(row + p0) = __builtin_shufflevector(t[s], t[s], 0, 1, 2, 3);
+        *(bf16x4*)(row + p1) = __builtin_shufflevector(t[s], t[s], 4, 5, 6, 7);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < SPLITS; ++s) *(bf16x8*)(buf + s * SK_TERM + c * SK_PITCH + kk) = t[s];
+    }
   }
 }
 
@@ -633,62 +649,82 @@ __device__ __forceinline__ void sk_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The six term products of a split pair on the 16x16x32 MFMA (smallest terms first,
+// as mfma_split)
+template <int SPLITS>
+__device__ __forceinline__ void mfma_split16(const bf16x8 (&a)[SPLITS], const bf16x8 (&b)[SPLITS],
+                                             f32x4 (&acc)[4], int rb) {
+  if (SPLITS == 3) {
+    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc[rb], 0, 0, 0);
+    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc[rb], 0, 0, 0);
+    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], acc[rb], 0, 0, 0);
+  }
+  acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc[rb], 0, 0, 0);
+  acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc[rb], 0, 0, 0);
+  acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc[rb], 0, 0, 0);
+}
+
 // C (n x RP, per matrix) = A (n x m) X, with X given transposed: XT (RP x ldxt),
 // XT[c][k] = X[k][c].  Needs m % 8 == 0.  asq: per-workgroup sums of squares of A.
-// Wave w owns rows r0 .. r0 + 63 (two 32-row MFMA blocks).  A is read 32 contraction
-// indices at a time: lane (l32, h) loads 16 consecutive floats of its two rows at
-// 32 j + 16 h, so each 128-byte line of A is requested by one instruction group; the
-// two k16 MFMA substeps of the step take the lane's floats 0-7 and 8-15 (contraction
-// order is free as long as the staged X fragments follow the same indices).
+// v_mfma_f32_16x16x32_bf16: lane l supplies row l%16 and 8 contraction indices of
+// each operand; the result D[4(l/16) + q][l%16] is acc[q].  The first operand is X
+// (D's rows are C's columns c), the second A (D's columns are rows i of A).
+// Wave w owns rows r0 .. r0 + 63 (four 16-row blocks rb) and all RP columns (four
+// 16-column blocks cb).  A is read 32 contraction indices (128 bytes of each row) per
+// step: lane (l16, g) loads the floats 4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3 of row
+// 16 rb + l16, so each load instruction covers 64 contiguous bytes of 16 rows (four
+// lanes per row).  The memory system serves that faster than the 32x32 MFMA's
+// layout, two lanes per row and 32 rows per instruction: a loads-only probe of the two
+// patterns over GPT-2-large's 72 x (5120 x 1280) fp32 ran 327 vs 400 us.  The lane's 8
+// indices per step are not consecutive; the staged X chunk is stored in the same order
+// (sk_stage_store<., true>), so the fragment of lane (l16, g) is 16 contiguous bytes.
 template <int SPLITS>
-__global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int n, int m,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void sk_rows(const float* __restrict__ A, int n, int m,
                                                const float* __restrict__ XT, int ldxt,
                                                float* __restrict__ C, double* __restrict__ asq) {
   __shared__ __attribute__((aligned(16))) bf16 xl[2 * SK_BUF];
   const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hk = lane >> 5;
+  const int l16 = lane & 15, g = lane >> 4;
   const int r0 = blockIdx.x * SKR_ROWS + wave * 64;
   A += (long long)b * n * m;
   XT += (long long)b * RP * ldxt;
   C += (long long)b * n * RP;
   const __amdgpu_buffer_rsrc_t ar = sk_rsrc(A, (long long)n * m);
   const __amdgpu_buffer_rsrc_t xr = sk_rsrc(XT, (long long)RP * ldxt);
-  bool ain[2];
-  unsigned abase[2];   // byte offset of the lane's first float, SK_OOB for rows >= n
+  unsigned abase[4];   // byte offset of the lane's first float, SK_OOB for rows >= n
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int i = r0 + 32 * rb + l32;
-    ain[rb] = i < n;
-    abase[rb] = ain[rb] ? (unsigned)(i * m + 16 * hk) * 4u : SK_OOB;
+  for (int rb = 0; rb < 4; ++rb) {
+    const int i = r0 + 16 * rb + l16;
+    abase[rb] = i < n ? (unsigned)(i * m + 4 * g) * 4u : SK_OOB;
   }
-  f32x16 acc[2][2];
+  f32x4 acc[4][4];   // [cb][rb]
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[rb][cb][e] = 0.f;
+      for (int e = 0; e < 4; ++e) acc[cb][rb][e] = 0.f;
   double sq = 0.0;
   const int nch = (m + SK_KC - 1) / SK_KC;  // staged chunks
-  // floats 8 q .. 8 q + 7 of the lane's 16 at step ks: indices 32 ks + 16 hk + 8 q ..
-  // (a step at or past nk loads zeros)
-  auto load = [&](int ks, float4 (&a)[2][4]) {
-    const int k = 32 * ks;
+  // the lane's floats of step ks: a[rb][h] = row 16 rb + l16, indices 32 ks + 16 h +
+  // 4 g .. + 3 (a group at or past m loads zeros; m % 4 == 0 keeps groups whole)
+  auto load = [&](int ks, float4 (&a)[4][2]) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const bool kin = k + 16 * hk + 4 * v < m;   // m % 8 == 0: 8-index groups are whole
+    for (int h = 0; h < 2; ++h) {
+      const int k = 32 * ks + 16 * h;
+      const bool kin = k + 4 * g < m;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-        a[rb][v] = sk_ld4(ar, kin ? abase[rb] + (unsigned)(k + 4 * v) * 4u : SK_OOB);
+      for (int rb = 0; rb < 4; ++rb)
+        a[rb][h] = sk_ld4(ar, kin ? abase[rb] + (unsigned)k * 4u : SK_OOB);
     }
   };
   SkStage stg;
   sk_stage_load(stg, xr, ldxt, 0, m, tid);
-  sk_stage_store<SPLITS>(stg, xl, tid);
+  sk_stage_store<SPLITS, true>(stg, xl, tid);
   sk_stage_load(stg, xr, ldxt, SK_KC, m, tid);
   // A two steps ahead: slot p holds step 2 ch + p (SK_KC / 32 == 2 steps per chunk)
   static_assert(SK_KC == 64, "two A slots per staged chunk");
-  float4 ab[2][2][4];
+  float4 ab[2][4][2];
   load(0, ab[0]);
   load(1, ab[1]);
   sk_barrier();
@@ -696,20 +732,21 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
     const bf16* buf = xl + (ch & 1) * SK_BUF;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      // a step past nk (the end of a partial last chunk) multiplies zeros
+      // a step past the end of a partial last chunk multiplies zeros
       const int ks = 2 * ch + p;
-      float4 ac[2][4];
+      float4 ac[4][2];
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) ac[rb][v] = sk_mov(ab[p][rb][v]);
+        for (int h = 0; h < 2; ++h) ac[rb][h] = sk_mov(ab[p][rb][h]);
       load(ks + 2, ab[p]);
+      // two row blocks at a time (the split terms of all four would cost occupancy)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        bf16x8 as[2][SPLITS], xs[2][SPLITS];
+      for (int rp = 0; rp < 4; rp += 2) {
+        bf16x8 as[2][SPLITS];
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          const float4 lo = ac[rb][2 * q], hi = ac[rb][2 * q + 1];
+        for (int u = 0; u < 2; ++u) {
+          const float4 lo = ac[rp + u][0], hi = ac[rp + u][1];
           const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
           if (asq) {
             float f = 0.f;
@@ -717,35 +754,35 @@ __global__ __launch_bounds__(256) void sk_rows(const float* __restrict__ A, int 
             for (int e = 0; e < 8; ++e) f = fmaf(v[e], v[e], f);
             sq += (double)f;
           }
-          split_bf16<SPLITS>(v, as[rb]);
+          split_bf16<SPLITS>(v, as[u]);
         }
-        sk_frags<SPLITS>(buf, 32 * p + 16 * hk + 8 * q, l32, xs);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int cb = 0; cb < 4; ++cb) {
+          bf16x8 xs[SPLITS];
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
-            acc[rb][cb] = mfma_split<SPLITS>(xs[cb], as[rb], acc[rb][cb]);
+          for (int s = 0; s < SPLITS; ++s)
+            xs[s] = *(const bf16x8*)(buf + s * SK_TERM + (16 * cb + l16) * SK_PITCH + 32 * p + 8 * g);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) mfma_split16<SPLITS>(xs, as[u], acc[cb], rp + u);
+        }
       }
     }
     // (after the last chunk this stages zeros nobody reads: no branch in the loop, so
     // the compiler keeps the prefetched loads in flight across iterations)
     sk_pin(stg);
-    sk_stage_store<SPLITS>(stg, xl + ((ch + 1) & 1) * SK_BUF, tid);
+    sk_stage_store<SPLITS, true>(stg, xl + ((ch + 1) & 1) * SK_BUF, tid);
     sk_barrier();
     sk_stage_load(stg, xr, ldxt, (ch + 2) * SK_KC, m, tid);
   }
-  // D[c][i] = C[i][c]: lane holds rows c = 32 cb + 8 g + 4 hk + q of column i = l32
+  // D[c][i] = C[i][c]: lane holds columns c = 16 cb + 4 g + q of row i = 16 rb + l16
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int i = r0 + 32 * rb + l32;
-    if (!ain[rb]) continue;
+  for (int rb = 0; rb < 4; ++rb) {
+    const int i = r0 + 16 * rb + l16;
+    if (i >= n) continue;
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *(float4*)&C[(long long)i * RP + 32 * cb + 8 * g + 4 * hk] =
-            make_float4(acc[rb][cb][4 * g], acc[rb][cb][4 * g + 1], acc[rb][cb][4 * g + 2],
-                        acc[rb][cb][4 * g + 3]);
+    for (int cb = 0; cb < 4; ++cb)
+      *(float4*)&C[(long long)i * RP + 16 * cb + 4 * g] =
+          make_float4(acc[cb][rb][0], acc[cb][rb][1], acc[cb][rb][2], acc[cb][rb][3]);
   }
   if (asq) {
     __shared__ double red[256];
