@@ -1461,33 +1461,42 @@ __device__ __forceinline__ void eh_inverse_iteration(int t0, int t1, int r, doub
   wave_lds_order();
 }
 
-// Z[t] <- Q Z[t] = H_0 H_1 ... H_{r-3} Z[t] for t < nvec, the last reflector first:
-// wave w takes vectors w, w + 8, ... (up to 4 at once, for independent reduction
-// chains), lane i row i; each reflector costs one DPP reduction per vector.
+// Z[t] <- Q Z[t] = H_0 H_1 ... H_{r-3} Z[t] for t < nvec, the last reflector first.
+// Eight lanes per vector, eight entries each (lane l: vector 8 wave + l / 8, entries
+// 8 (l % 8) .. +7), so a wave carries 8 vectors and each reflector's dot product is 8
+// fmas and a reduction over 8 lanes in 3 DPP steps.  (One vector per wave, one entry
+// per lane and a 64-lane reduction per reflector took ~30 us for 8 vectors.)
 __device__ __forceinline__ void eh_back_transform(int nvec, int r, const double* taus,
                                                   const double* Vr, double* Z, int wave, int l) {
-  for (int t0 = wave; t0 < nvec; t0 += 4 * EH_WAVES) {
-    double z[4];
+  if (8 * wave >= nvec) return;   // uniform over the wave
+  const int t = 8 * wave + (l >> 3), e0 = 8 * (l & 7);
+  const bool live = t < nvec;
+  double z[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int t = t0 + q * EH_WAVES;
-      z[q] = t < nvec ? Z[t * ZP + l] : 0.0;
-    }
-    for (int k = r - 3; k >= 0; --k) {
-      const double tk = taus[k];
-      if (tk == 0.0) continue;
-      const double vi = Vr[k * RP + l];   // zero for rows <= k and past r
+  for (int c = 0; c < 8; ++c) z[c] = live ? Z[t * ZP + e0 + c] : 0.0;
+  for (int k = r - 3; k >= 0; --k) {
+    const double tk = taus[k];
+    if (tk == 0.0) continue;
+    double v[8];   // reflector k: zero for entries <= k and past r
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const double sq = wave_sum_d(vi * z[q]) * tk;
-        z[q] = fma(-sq, vi, z[q]);
-      }
-    }
+    for (int c = 0; c < 8; ++c) v[c] = Vr[k * RP + e0 + c];
+    double s0 = v[0] * z[0], s1 = v[1] * z[1];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int t = t0 + q * EH_WAVES;
-      if (t < nvec) Z[t * ZP + l] = z[q];
+    for (int c = 2; c < 8; c += 2) {
+      s0 = fma(v[c], z[c], s0);
+      s1 = fma(v[c + 1], z[c + 1], s1);
     }
+    double sq = s0 + s1;
+    sq += dpp_d(sq, 0);   // pairs
+    sq += dpp_d(sq, 1);   // quads
+    sq += dpp_d(sq, 2);   // the 8 lanes of the vector (half-row mirror)
+    sq *= tk;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) z[c] = fma(-sq, v[c], z[c]);
+  }
+  if (live) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) Z[t * ZP + e0 + c] = z[c];
   }
 }
 
