@@ -510,9 +510,8 @@ __device__ __forceinline__ void gram_mfma(const float4 (&v)[GRAM_G], f64x4 (&acc
   }
 }
 
-__global__ __launch_bounds__(64) void gram_partials(const float* __restrict__ Y, int rows,
-                                                    long long y_bs, double* __restrict__ part) {
-  const int b = blockIdx.y, chunk = blockIdx.x, l = threadIdx.x;
+__device__ __forceinline__ void gram_chunk(const float* __restrict__ Y, int rows, long long y_bs,
+                                           double* __restrict__ part, int b, int chunk, int l) {
   const int per = (rows + GRAM_CHUNKS - 1) / GRAM_CHUNKS;
   const int lo = chunk * per, hi = min(rows, lo + per);
   const __amdgpu_buffer_rsrc_t yr = sk_rsrc(Y + (long long)b * y_bs, (long long)rows * RP);
@@ -554,6 +553,25 @@ __global__ __launch_bounds__(64) void gram_partials(const float* __restrict__ Y,
         out[p * RP + q] = acc[t][e];
         if (c != c2) out[q * RP + p] = acc[t][e];
       }
+}
+
+// grid (GRAM_CHUNKS, batch)
+__global__ __launch_bounds__(64) void gram_partials(const float* __restrict__ Y, int rows,
+                                                    long long y_bs, double* __restrict__ part) {
+  gram_chunk(Y, rows, y_bs, part, blockIdx.y, blockIdx.x, threadIdx.x);
+}
+
+// two independent Gram partials in one launch (Bp Bp^T and Q^T Q before the gate):
+// grid (2 GRAM_CHUNKS, batch)
+__global__ __launch_bounds__(64) void gram_partials_pair(const float* __restrict__ Y1, int rows1,
+                                                         double* __restrict__ part1,
+                                                         const float* __restrict__ Y2, int rows2,
+                                                         double* __restrict__ part2) {
+  if ((int)blockIdx.x < GRAM_CHUNKS)
+    gram_chunk(Y1, rows1, (long long)rows1 * RP, part1, blockIdx.y, blockIdx.x, threadIdx.x);
+  else
+    gram_chunk(Y2, rows2, (long long)rows2 * RP, part2, blockIdx.y, blockIdx.x - GRAM_CHUNKS,
+               threadIdx.x);
 }
 
 // A copy the compiler cannot fold away: a prefetch slot is copied out before its next
@@ -2301,9 +2319,14 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
                  (long long)m * RP)))
       return rc;
   }
-  // H = Bp Bp^T = Gram of Bp^T
-  if ((rc = gram(st, w.Bt, B, m, w.gram))) return rc;
-  if (d && (rc = gram(st, w.Q, B, n, w.gramq))) return rc;
+  // H = Bp Bp^T = Gram of Bp^T (and Q^T Q for d, in the same launch)
+  if (d) {
+    hipLaunchKernelGGL(gram_partials_pair, dim3(2 * GRAM_CHUNKS, B), dim3(64), 0, st, w.Bt, m,
+                       w.gram, w.Q, n, w.gramq);
+    DMH_CHECK_LAUNCH("gram_partials (Bp, Q)");
+  } else if ((rc = gram(st, w.Bt, B, m, w.gram))) {
+    return rc;
+  }
   if (d && gp.thresh >= gp.ratio) {
     // clip / fused paths: the head eigenpairs only (with the clip threshold at or above
     // the gate ratio, every deflated direction lies within the gate window)
