@@ -270,36 +270,66 @@ __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restric
   for (int c = 0; c < CW; ++c) Ls[l * LP + CW * wave + c] = g[c];
   if (fail) s_fail = 1;
   __syncthreads();
-  if (tid >= 64) return;
   fail = s_fail != 0;
-  // x = column l of L^-1 by forward substitution,
-  // L[i][i] x_i = delta_il - sum_{t<i} L[i][t] x_t (broadcast reads of row i of L);
-  // x_i = 0 for i < l
-  double x[RP];
+  // x = column l of L^-1 (lane l) by forward substitution,
+  // L[i][i] x_i = delta_il - sum_{t<i} L[i][t] x_t, x_i = 0 for i < l, blocked by the
+  // waves' rows: wave w holds rows CW w .. CW w + CW - 1 of every column.  Block J: wave J
+  // solves its rows (the terms of its own block) and publishes them in LDS; after one
+  // barrier the later waves subtract the block's terms from their rows' sums.  Each sum
+  // takes its terms in the same order as a one-lane loop over t (even t in s0, odd t in
+  // s1), so the inverse is bit-identical to it (16 -> ~4 us).
+  double* const Xs = Lc;   // (Lc is free once L is in Ls by rows)
+  double s0[CW], s1[CW], xr[CW];
 #pragma unroll
-  for (int i = 0; i < RP; ++i) {
-    double s0 = (i == l) ? 1.0 : 0.0, s1 = 0.0;
+  for (int q = 0; q < CW; ++q) {
+    s0[q] = (CW * wave + q == l) ? 1.0 : 0.0;
+    s1[q] = 0.0;
+    xr[q] = 0.0;
+  }
+  for (int J = 0; J < CHOL_THREADS / 64; ++J) {
+    if (wave == J) {
 #pragma unroll
-    for (int t = 0; t + 1 < i; t += 2) {
-      s0 = fma(-Ls[i * LP + t], x[t], s0);
-      s1 = fma(-Ls[i * LP + t + 1], x[t + 1], s1);
-      if ((t & 7) == 6) asm volatile("" ::: "memory");   // row loads in batches of 8
+      for (int q = 0; q < CW; ++q) {
+        const int i = CW * J + q;
+#pragma unroll
+        for (int t2 = 0; t2 < q; ++t2) {
+          const double lit = Ls[i * LP + CW * J + t2];
+          if (t2 & 1) s1[q] = fma(-lit, xr[t2], s1[q]);
+          else s0[q] = fma(-lit, xr[t2], s0[q]);
+        }
+        xr[q] = (i < l) ? 0.0 : (s0[q] + s1[q]) * Ld[i];
+        Xs[i * RP + l] = xr[q];
+      }
     }
-    if (i & 1) s0 = fma(-Ls[i * LP + i - 1], x[i - 1], s0);
-    x[i] = (i < l) ? 0.0 : (s0 + s1) * Ld[i];
-  }
-  // M = L^-T: M[a][c] = (L^-1)[c][a], so row l of M is x
-  float* Mb = M + (long long)b * RP * RP + (long long)l * RP;
+    __syncthreads();
+    if (wave > J) {
 #pragma unroll
-  for (int c = 0; c < RP; c += 4) {
-    float4 v;
-    v.x = (!fail && l < r && c < r) ? (float)x[c] : 0.f;
-    v.y = (!fail && l < r && c + 1 < r) ? (float)x[c + 1] : 0.f;
-    v.z = (!fail && l < r && c + 2 < r) ? (float)x[c + 2] : 0.f;
-    v.w = (!fail && l < r && c + 3 < r) ? (float)x[c + 3] : 0.f;
-    *(float4*)&Mb[c] = v;
+      for (int t2 = 0; t2 < CW; ++t2) {
+        const int t = CW * J + t2;
+        const double xt = Xs[t * RP + l];
+#pragma unroll
+        for (int q = 0; q < CW; ++q) {
+          const double lit = Ls[(CW * wave + q) * LP + t];
+          if (t2 & 1) s1[q] = fma(-lit, xt, s1[q]);
+          else s0[q] = fma(-lit, xt, s0[q]);
+        }
+      }
+    }
   }
-  if (l == 0 && degen && fail) degen[b] = 1;
+  static_assert(CW % 4 == 0, "the rows of a wave go out as whole float4s");
+  // M = L^-T: M[a][c] = (L^-1)[c][a], so row l of M is x; wave w writes its CW entries
+  float* Mb = M + (long long)b * RP * RP + (long long)l * RP + CW * wave;
+#pragma unroll
+  for (int q = 0; q < CW; q += 4) {
+    const int c = CW * wave + q;
+    float4 v;
+    v.x = (!fail && l < r && c < r) ? (float)xr[q] : 0.f;
+    v.y = (!fail && l < r && c + 1 < r) ? (float)xr[q + 1] : 0.f;
+    v.z = (!fail && l < r && c + 2 < r) ? (float)xr[q + 2] : 0.f;
+    v.w = (!fail && l < r && c + 3 < r) ? (float)xr[q + 3] : 0.f;
+    *(float4*)&Mb[q] = v;
+  }
+  if (tid == 0 && degen && fail) degen[b] = 1;
 }
 
 // C (rows x RP) = Y (rows x RP) * M (RP x RP), per matrix; 64 rows per workgroup,
