@@ -10,9 +10,14 @@
 // Kernels:
 //   skinny_gemm<ROWS>   C = A X       (n x RP)   fp32 MFMA 32x32x2, A streamed by rows
 //   skinny_gemm<COLS>   C = A^T Y     (m x RP)   fp32 MFMA 32x32x2, A streamed by columns
-//   gram_partials       partial fp64 Gram Y^T Y over row chunks
-//   chol_inv            sum partials, Cholesky in LDS (fp64, columns over 8 waves),
-//                       M = L^-T  (one workgroup)
+//                       (both for the shapes sk_fast() leaves out: n or m not a
+//                       multiple of 8, or a matrix of 2 GiB or more)
+//   sk_rows             C = A X       (n x RP)   split-bf16 MFMA 16x16x32, X staged in LDS
+//   sk_cols, sk_reduce  C = A^T Y     (m x RP)   split-bf16 MFMA 32x32x16, row-split partials
+//   gram_partials       partial fp64 Gram Y^T Y over row chunks (gram_partials_pair: two)
+//   chol_inv            sum partials, Cholesky in LDS (fp64, blocked by 8-column
+//                       panels over 8 waves), M = L^-T by blocked forward
+//                       substitution  (one workgroup)
 //   right_mult          C = Y M       (rows x RP) x (RP x RP)
 //   eig_gate            Jacobi eigen-decomposition of Bp Bp^T in LDS (fp64) -> s, Ub;
 //                       the deflation gate and the per-column deflate/restore weights
@@ -226,7 +231,7 @@ __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restric
   // multipliers by readlane) and publishes them in rows CW p .. of Lc; after one barrier
   // the waves of later panels apply the CW new columns to theirs.  Every element sees
   // the same operations in the same order as in a one-wave loop over k (one barrier per
-  // panel instead of one per pivot: 25 -> ~8 us).
+  // panel instead of one per pivot: 25 -> 11 us per workgroup).
   constexpr int CW = RP / (CHOL_THREADS / 64);   // columns per wave
   static_assert(RP % (CHOL_THREADS / 64) == 0, "the waves share the columns evenly");
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -277,7 +282,7 @@ __global__ __launch_bounds__(CHOL_THREADS) void chol_inv(const double* __restric
   // solves its rows (the terms of its own block) and publishes them in LDS; after one
   // barrier the later waves subtract the block's terms from their rows' sums.  Each sum
   // takes its terms in the same order as a one-lane loop over t (even t in s0, odd t in
-  // s1), so the inverse is bit-identical to it (16 -> ~4 us).
+  // s1), so the inverse is bit-identical to it (16 -> 6 us per workgroup).
   double* const Xs = Lc;   // (Lc is free once L is in Ls by rows)
   double s0[CW], s1[CW], xr[CW];
 #pragma unroll
