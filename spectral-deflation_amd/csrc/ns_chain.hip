@@ -469,8 +469,13 @@ void gemm_nt_bf16(GemmArgs g) {
     //     128-byte lines (8 rows j x 64 i).  (Half-line stores of a transposed
     //     32-row block made the next launch's reads of those lines slow: the chain
     //     ran 10% longer.)
-    // Row-pass staging element (r, c) sits at byte r*128 + 16*((c>>3) ^ (r&7)) +
-    // 2*(c&7); transposed-pass element (i, j) at i*64 + 8*((j>>2) ^ (i&7)) + 2*(j&3).
+    // Row-pass staging element (r, c) sits at byte rpos(r, c>>3) + 2*(c&7), the 16-byte
+    // chunks of a row XOR-swizzled by r&7 and r>>4; transposed-pass element (i, j) at
+    // tpos(i, j>>2) + 2*(j&3), the 64-byte rows permuted by i ^ (i>>3 & 3) and the 8-byte
+    // units swizzled by i&7 and bits 4-5 of i.  With 32 or with 64 four-byte LDS banks the
+    // transposed pass's 8-byte writes and reads are then conflict free (an unswizzled
+    // read of 8 rows i = 8a + q by 8 consecutive lanes hit one bank 8 times) and the
+    // row pass's 8-byte writes at most 2-way (4-way with the r&7 swizzle alone).
     // acc[i][j][4g+q] holds C[32 i + (lane&31)][32 j + 8g + 4(lane>>5) + q] of the
     // wave tile.
     // Diagonal tiles of a symmetric product are stored whole, row-major: the MFMAs
@@ -478,6 +483,10 @@ void gemm_nt_bf16(GemmArgs g) {
     {
       const int wi0 = ti * TILE + WT_M * wm, wj0 = tj * TILE + WT_N * wn;
       const bool diag = g.sym && ti == tj;
+      auto rpos = [](int r, int ch) { return r * 128 + 16 * (ch ^ (r & 7) ^ ((r >> 4) & 1)); };
+      auto tpos = [](int i, int u) {
+        return (i ^ ((i >> 3) & 3)) * 64 + 8 * (u ^ (i & 7) ^ ((i >> 2) & 4) ^ (((i >> 5) & 1) * 6));
+      };
       bf16* outb = g.out ? g.out + (long long)b * g.out_bs : nullptr;
       bf16* outtb = g.outT && !diag ? g.outT + (long long)b * g.outT_bs : nullptr;
       const bool al_out = g.out_rows > 0 || (g.out_ld & 7) == 0;
@@ -528,7 +537,7 @@ void gemm_nt_bf16(GemmArgs g) {
               o[q] = f2bf(EPI == EPI_POLY ? g.beta * v : v);
             }
             const int ch = 4 * bj + gq;
-            *(bf16x4*)(stg + r32 * 128 + 16 * (ch ^ (r32 & 7)) + 8 * hi) = o;
+            *(bf16x4*)(stg + rpos(r32, ch) + 8 * hi) = o;
           }
         }
         if (EPI == EPI_POLY && bi + AUX_AHEAD < BM) load_aux(bi + AUX_AHEAD);
@@ -537,7 +546,7 @@ void gemm_nt_bf16(GemmArgs g) {
         for (int v = 0; v < 4; ++v) {
           const int u = lane + 64 * v;
           const int r = u >> 3, ch = u & 7;
-          char* lp = stg + r * 128 + 16 * (ch ^ (r & 7));
+          char* lp = stg + rpos(r, ch);
           bf16x8 val = *(const bf16x8*)lp;
           const int gi = i0 + r, gj = wj0 + 8 * ch;
           if (EPI == EPI_POLY) {
@@ -561,7 +570,7 @@ void gemm_nt_bf16(GemmArgs g) {
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
               const int ch = 4 * bj + gq;
-              const bf16x4 o = *(const bf16x4*)(stg + r32 * 128 + 16 * (ch ^ (r32 & 7)) + 8 * hi);
+              const bf16x4 o = *(const bf16x4*)(stg + rpos(r32, ch) + 8 * hi);
 #pragma unroll
               for (int q = 0; q < 4; ++q) acc[bi][bj][4 * gq + q] = bf2f(o[q]);
             }
@@ -584,14 +593,14 @@ void gemm_nt_bf16(GemmArgs g) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) o[q] = f2bf(acc[2 * bp + h][bj][4 * gq + q]);
                 const int i = 32 * h + r32, unit = 2 * gq + hi;
-                *(bf16x4*)(stg + i * 64 + 8 * (unit ^ (i & 7))) = o;
+                *(bf16x4*)(stg + tpos(i, unit)) = o;
               }
             }
             uint2 rr[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
               const int i = 8 * a + q;
-              rr[q] = *(const uint2*)(stg + i * 64 + 8 * (c ^ q));
+              rr[q] = *(const uint2*)(stg + tpos(i, c));
             }
             const int gi = wi0 + 64 * bp + 8 * a;
 #pragma unroll
