@@ -541,26 +541,37 @@ void gemm_nt_bf16(GemmArgs g) {
           }
         }
         if (EPI == EPI_POLY && bi + AUX_AHEAD < BM) load_aux(bi + AUX_AHEAD);
-        // phase 2
+        // phase 2: plain stores read a lane's chunks two at a time, so two LDS reads
+        // share one wait (not a read-wait-store chain per chunk; four at a time spill
+        // registers in K3, and POLY, shorter still, reads each chunk where it uses
+        // it); whole wave tiles store without masks or branches
+        bf16x8 val[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int u = lane + 64 * v;
           const int r = u >> 3, ch = u & 7;
-          char* lp = stg + rpos(r, ch);
-          bf16x8 val = *(const bf16x8*)lp;
+          if (EPI == EPI_POLY) val[v] = *(const bf16x8*)(stg + rpos(r, ch));
+          else if ((v & 1) == 0) {
+            val[v] = *(const bf16x8*)(stg + rpos(r, ch));
+            val[v + 1] = *(const bf16x8*)(stg + rpos((u + 64) >> 3, (u + 64) & 7));
+          }
           const int gi = i0 + r, gj = wj0 + 8 * ch;
           if (EPI == EPI_POLY) {
             const int qd = diag && gi < g.diag_lim ? gi - gj : -1;   // the diagonal's slot, if here
 #pragma unroll
             for (int q = 0; q < 8; ++q)
-              val[q] = f2bf(g.alpha * bf2f(av[EPI == EPI_POLY ? bi : 0][v][q]) + bf2f(val[q]) +
-                            (q == qd ? g.diag_add : 0.f));
-            if (outtb) *(bf16x8*)lp = val;
+              val[v][q] = f2bf(g.alpha * bf2f(av[EPI == EPI_POLY ? bi : 0][v][q]) + bf2f(val[v][q]) +
+                               (q == qd ? g.diag_add : 0.f));
+            if (outtb) *(bf16x8*)(stg + rpos(r, ch)) = val[v];
           }
-          if (outb && gi < g.valid_i) {
-            unsigned mask = 0xffu;
-            if (gj + 8 > g.valid_j) mask = gj >= g.valid_j ? 0u : (1u << (g.valid_j - gj)) - 1u;
-            if (mask) store8(outb + out_off(gi, gj), val, mask, al_out);
+          if (outb) {
+            if (whole) {
+              __builtin_nontemporal_store(val[v], (bf16x8*)(outb + out_off(gi, gj)));
+            } else if (gi < g.valid_i) {
+              unsigned mask = 0xffu;
+              if (gj + 8 > g.valid_j) mask = gj >= g.valid_j ? 0u : (1u << (g.valid_j - gj)) - 1u;
+              if (mask) store8(outb + out_off(gi, gj), val[v], mask, al_out);
+            }
           }
         }
         // phase 2b: POLY's stored values back into acc (the inverse of phase 1)
@@ -616,13 +627,16 @@ void gemm_nt_bf16(GemmArgs g) {
                 const uint32_t hw = (cc & 1) ? (x1 & 0xffff0000u) : (x1 << 16);
                 w[h] = lo | hw;
               }
+              const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
+              if (whole) {
+                __builtin_nontemporal_store(__builtin_bit_cast(bf16x8, wv),
+                                            (bf16x8*)(outtb + outT_off(gj, gi)));
+                continue;
+              }
               if (gj >= g.valid_j) continue;
               unsigned mask = 0xffu;
               if (gi + 8 > g.valid_i) mask = gi >= g.valid_i ? 0u : (1u << (g.valid_i - gi)) - 1u;
-              if (mask) {
-                const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
-                store8(outtb + outT_off(gj, gi), __builtin_bit_cast(bf16x8, wv), mask, al_outT);
-              }
+              if (mask) store8(outtb + outT_off(gj, gi), __builtin_bit_cast(bf16x8, wv), mask, al_outT);
             }
           }
         }
