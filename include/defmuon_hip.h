@@ -48,6 +48,9 @@ const char* dmh_last_error(void);
  *   entry_mode   0: x used as is; 1: x / (||x||_F + 1e-7); 2: x / (1.01 ||x||_F + 1e-7)
  *                (norm per matrix over the un-rounded input)
  *   coeffs       steps x 3 doubles (a, b, c) per step
+ * Limit: the padded iterate (rows and cols rounded up to multiples of 256, bf16) must
+ * stay below 2^31 bytes (32-bit operand addressing); larger shapes return 1.  The
+ * same limit applies to the chain of dmh_deflated_polar*.
  */
 int dmh_ns_workspace_size(int batch, int rows, int cols, int orient_tall, size_t* bytes);
 int dmh_ns_chain(dmh_stream_t stream, const void* x, int x_dtype, int batch, int rows, int cols,
@@ -59,7 +62,10 @@ int dmh_ns_chain(dmh_stream_t stream, const void* x, int x_dtype, int batch, int
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments
  * without the workspace, which is a static device array of DMH_NS_SCRATCH_BYTES
- * (64 MiB) per GPU, held from the first call on that GPU until the process ends.
+ * (64 MiB) per GPU.  The array belongs to the library's code object, which the HIP
+ * runtime loads on a GPU when any of the library's kernels first runs there: every
+ * process that uses the library holds 64 MiB of HBM on each GPU it runs on until it
+ * ends, whether or not it calls this entry.
  * A shape whose workspace (dmh_ns_workspace_size) exceeds it returns 2.  Every call
  * on one GPU uses the same array: calls that overlap on one GPU race. */
 #define DMH_NS_SCRATCH_BYTES (64u << 20)
@@ -184,8 +190,8 @@ int dmh_apply_update(dmh_stream_t stream, const dmh_glue_param* params, int coun
  * the same order.  `table` (device memory, `count` entries) lists the group's
  * parameters; `chunk_start` (device memory, count + 1 ints) gives each parameter's
  * first chunk of dmh_adamw_chunks-sized work, chunk_start[count] = nchunks.  The
- * caller keeps both arrays (the tensors do not move between steps), so a step
- * allocates and copies nothing.  w1 = 1 - beta1, w2 = 1 - beta2, decay = 1 - lr*wd,
+ * caller keeps both arrays while the tensors stay at the same addresses, so such a
+ * step allocates and copies nothing.  w1 = 1 - beta1, w2 = 1 - beta2, decay = 1 - lr*wd,
  * alpha = -lr/scale with scale the bias correction of the (common) step count. */
 typedef struct {
   float* param;        /* updated in place */

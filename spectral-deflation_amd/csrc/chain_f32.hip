@@ -1,14 +1,19 @@
 // fp32 tall-convention polynomial chain (the dtype-preserving path of
 //   _horner_iterate   defmuon/optim/deflation_batched.py:196-204
-// for fp32 input: G = X^T X;  B = b G + (c G) G;  X <- a X + X B, all in fp32).
+// for fp32 input: G = X^T X;  B = b G + (c G) G;  X <- a X + X B, all in fp32, with the
+// reference's rounding points: c G and b G rounded on their own, each sum of two
+// rounded terms rounded once; only the products' summation order differs).
 //
 // The bf16 chain (ns_chain.hip) is the training path; this one serves callers that
 // hand the iteration fp32 matrices (the reference's own convergence study runs it in
 // fp32), one launch per GEMM phase over the batch.  Each phase is
-//   C[i][j] = alpha * sum_k P(i, k) Q(j, k) + beta * R[i][j]
-// with P and Q read through element strides, so T^T T, G G and X B need no
-// transposed copies.  64 x 64 output tiles, 16-deep K slices staged in LDS, 4 x 4
-// outputs per thread accumulated in k order with fp32 FMAs.
+//   C[i][j] = fl(fl(beta * R[i][j]) + fl(sum_k fl(s * P(i, k)) Q(j, k)))
+// (the R term only where beta != 0, the scale s of P applied as its K slices are
+// staged) with P and Q read through element strides, so T^T T, (c G) G and X B need
+// no transposed copies.  64 x 64 output tiles, 16-deep K slices staged in LDS, 4 x 4
+// outputs per thread accumulated in k order with fp32 FMAs.  (MI355X's fp32 matrix
+// cores have the same 157.3 TFLOP/s peak as its fp32 vector units, so this path
+// stays on the VALU.)
 #include "common.h"
 
 namespace dmh {
@@ -18,31 +23,33 @@ constexpr int F_BK = 16;
 
 struct F32Gemm {
   const float* P; long long p_bs; int p_si, p_sk;   // P(i, k) = P[b*p_bs + i*p_si + k*p_sk]
+  float p_scale;                                     // staged as fl(p_scale * P(i, k))
   const float* Q; long long q_bs; int q_sj, q_sk;   // Q(j, k)
   const float* R; long long r_bs; int r_ld;         // R[i][j] (beta != 0 only)
   float* C; long long c_bs; int c_ld;               // C[i][j]
   int I, J, K;
-  float alpha, beta;
+  float beta;
 };
 
-// one K slice of a 64-row operand panel into LDS, S[k][row]; coalesced along the
-// operand's unit-stride index
+// one K slice of a 64-row operand panel into LDS, S[k][row] = fl(scale * operand);
+// coalesced along the operand's unit-stride index
 __device__ __forceinline__ void f32_stage(float (*S)[F_TILE + 4], const float* base, int si,
-                                          int sk, int r0, int rows, int k0, int K) {
+                                          int sk, int r0, int rows, int k0, int K,
+                                          float scale) {
   const int t = threadIdx.x;
   if (si == 1) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int r = t & 63, k = (t >> 6) + 4 * u;
       const int gr = r0 + r, gk = k0 + k;
-      S[k][r] = (gr < rows && gk < K) ? base[(long long)gr * si + (long long)gk * sk] : 0.f;
+      S[k][r] = (gr < rows && gk < K) ? __fmul_rn(scale, base[(long long)gr * si + (long long)gk * sk]) : 0.f;
     }
   } else {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int k = t & 15, r = (t >> 4) + 16 * u;
       const int gr = r0 + r, gk = k0 + k;
-      S[k][r] = (gr < rows && gk < K) ? base[(long long)gr * si + (long long)gk * sk] : 0.f;
+      S[k][r] = (gr < rows && gk < K) ? __fmul_rn(scale, base[(long long)gr * si + (long long)gk * sk]) : 0.f;
     }
   }
 }
@@ -57,8 +64,8 @@ __global__ __launch_bounds__(256) void gemm_f32(F32Gemm g) {
   const int ti = threadIdx.x >> 4, tj = threadIdx.x & 15;
   float acc[4][4] = {};
   for (int k0 = 0; k0 < g.K; k0 += F_BK) {
-    f32_stage(Ps, P, g.p_si, g.p_sk, i0, g.I, k0, g.K);
-    f32_stage(Qs, Q, g.q_sj, g.q_sk, j0, g.J, k0, g.K);
+    f32_stage(Ps, P, g.p_si, g.p_sk, i0, g.I, k0, g.K, g.p_scale);
+    f32_stage(Qs, Q, g.q_sj, g.q_sk, j0, g.J, k0, g.K, 1.f);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < F_BK; ++k) {
@@ -82,8 +89,8 @@ __global__ __launch_bounds__(256) void gemm_f32(F32Gemm g) {
     for (int y = 0; y < 4; ++y) {
       const int j = j0 + 4 * tj + y;
       if (j >= g.J) continue;
-      float v = g.alpha * acc[x][y];
-      if (R) v = fmaf(g.beta, R[(long long)i * g.r_ld + j], v);
+      float v = acc[x][y];
+      if (R) v = __fadd_rn(__fmul_rn(g.beta, R[(long long)i * g.r_ld + j]), v);
       C[(long long)i * g.c_ld + j] = v;
     }
   }
@@ -151,13 +158,13 @@ int dmh_horner_f32(hipStream_t stream, const float* x, int batch, int n, int m, 
     float* dst = ((steps - 1 - it) % 2 == 0) ? out : tmp;   // the last step lands in out
     int rc;
     // G = X^T X: P(i, k) = Q(i, k) = X[k][i]
-    F32Gemm g1{src, tsz, 1, m, src, tsz, 1, m, nullptr, 0, 0, G, gsz, m, m, m, n, 1.f, 0.f};
+    F32Gemm g1{src, tsz, 1, m, 1.f, src, tsz, 1, m, nullptr, 0, 0, G, gsz, m, m, m, n, 0.f};
     if ((rc = launch_f32(g1, batch, stream, "dmh_horner_f32 G"))) return rc;
-    // B = c G G + b G: P(i, k) = G[i][k], Q(j, k) = G[k][j]
-    F32Gemm g2{G, gsz, m, 1, G, gsz, 1, m, G, gsz, m, Bm, gsz, m, m, m, m, c, b};
+    // B = b G + (c G) G: P(i, k) = c G[i][k], Q(j, k) = G[k][j]
+    F32Gemm g2{G, gsz, m, 1, c, G, gsz, 1, m, G, gsz, m, Bm, gsz, m, m, m, m, b};
     if ((rc = launch_f32(g2, batch, stream, "dmh_horner_f32 B"))) return rc;
-    // X' = X B + a X: P(i, k) = X[i][k], Q(j, k) = B[k][j]
-    F32Gemm g3{src, tsz, m, 1, Bm, gsz, 1, m, src, tsz, m, dst, tsz, m, n, m, m, 1.f, a};
+    // X' = a X + X B: P(i, k) = X[i][k], Q(j, k) = B[k][j]
+    F32Gemm g3{src, tsz, m, 1, 1.f, Bm, gsz, 1, m, src, tsz, m, dst, tsz, m, n, m, m, a};
     if ((rc = launch_f32(g3, batch, stream, "dmh_horner_f32 X"))) return rc;
     src = dst;
   }

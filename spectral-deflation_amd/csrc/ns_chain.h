@@ -38,6 +38,9 @@ struct ChainWs {
 };
 
 ChainDims chain_dims(int rows, int cols, int orient_tall);
+// DMH_OK, or DMH_EINVAL (with the error text) when a padded operand reaches 2^31
+// bytes: the GEMMs address their operands through 32-bit buffer descriptors and offsets
+int chain_check(const char* what, const ChainDims& d);
 ChainWs chain_ws(void* ws, int batch, const ChainDims& d);   // ws == nullptr: sizes only
 
 // Run `steps` iterations from T0 already packed in the workspace; the result

@@ -439,6 +439,10 @@ void gemm_nt_bf16(GemmArgs g) {
     // stays in flight under the epilogue.
     const int nkofs = (g.kspread * (nti + ntj)) % nk;
     if (more) DMH_GLOAD(rPn, rQn, nkofs * TK, s_cur ^ 1);
+    // Nothing may be scheduled across this point: the next tile's first wait counts
+    // on exactly vm_after vector memory instructions (the epilogue's aux loads and
+    // stores) following these loads in program order.
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     {
       const char* cur = smem + s_cur * STAGEB;
@@ -505,9 +509,9 @@ void gemm_nt_bf16(GemmArgs g) {
       const bool whole = wi0 + WT_M <= g.valid_i && wj0 + WT_N <= g.valid_j &&
                          (!outb || al_out) && (!outtb || al_outT);
       vm_after = whole ? (outb ? 16 : 0) + (outtb ? 16 : 0) + (EPI == EPI_POLY ? 16 : 0) : -1;
-      // POLY: the aux of block rows 0 and 1 is requested up front and that of row
-      // bi+2 once row bi's accumulators are drained, so the reads run two block rows
-      // ahead of their use (latency hidden, registers bounded)
+      // POLY: the aux of block row 0 is requested up front and that of row bi+1 once
+      // row bi's accumulators are staged, so the reads run one block row ahead of
+      // their use (latency hidden under the staging, registers bounded)
       constexpr int AUX_AHEAD = 1;
       bf16x8 av[EPI == EPI_POLY ? BM : 1][4];
       auto load_aux = [&](int bi) {
@@ -835,6 +839,18 @@ ChainDims chain_dims(int rows, int cols, int orient_tall) {
   return d;
 }
 
+int chain_check(const char* what, const ChainDims& d) {
+  // the largest operand is the padded iterate T (np x mp bf16, np >= mp); its buffer
+  // descriptor's record count and the loaders' byte offsets are 32-bit
+  if ((long long)d.np * d.mp * (long long)sizeof(bf16) >= (1LL << 31)) {
+    set_error("%s: a %d x %d matrix pads to %d x %d bf16 = %lld bytes, beyond the chain's "
+              "32-bit operand addressing (< 2^31 bytes)", what, d.n, d.m, d.np, d.mp,
+              (long long)d.np * d.mp * (long long)sizeof(bf16));
+    return DMH_EINVAL;
+  }
+  return DMH_OK;
+}
+
 ChainWs chain_ws(void* ws, int batch, const ChainDims& d) {
   ChainWs w{};
   const size_t tw = (size_t)batch * d.np * d.mp;
@@ -965,7 +981,9 @@ int dmh_ns_workspace_size(int batch, int rows, int cols, int orient_tall, size_t
     set_error("dmh_ns_workspace_size: bad arguments");
     return DMH_EINVAL;
   }
-  *bytes = chain_ws(nullptr, batch, chain_dims(rows, cols, orient_tall)).bytes;
+  const ChainDims d = chain_dims(rows, cols, orient_tall);
+  if (chain_check("dmh_ns_workspace_size", d)) return DMH_EINVAL;
+  *bytes = chain_ws(nullptr, batch, d).bytes;
   return DMH_OK;
 }
 
@@ -982,6 +1000,7 @@ int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int 
     return DMH_EINVAL;
   }
   const ChainDims d = chain_dims(rows, cols, orient_tall);
+  if (chain_check("dmh_ns_chain", d)) return DMH_EINVAL;
   const ChainWs w = chain_ws(ws, batch, d);
   if (!ws || ws_bytes < w.bytes) {
     set_error("dmh_ns_chain: workspace %zu < %zu bytes", ws_bytes, w.bytes);
@@ -1005,7 +1024,8 @@ int dmh_ns_chain(hipStream_t stream, const void* x, int x_dtype, int batch, int 
 // dmh_ns_chain_noalloc: dmh_ns_chain with its workspace in a static device array
 // (for callers that cannot allocate: code under HIP graph capture, serving loops,
 // harnesses that forbid hipMalloc).  Each GPU holds its own copy of the array from
-// the first call on it until the process ends.  The array's host-side name is not a
+// the moment the library's code object is loaded there (the first launch of any of
+// its kernels on that GPU) until the process ends, whether or not this entry is used.  The array's host-side name is not a
 // device address: its address on the current device comes from hipGetSymbolAddress,
 // once per device, and only that pointer is handed to kernels.  Every call on a GPU
 // uses the same array, so calls that overlap on one GPU (other streams, other
@@ -1051,7 +1071,9 @@ extern "C" int dmh_ns_chain_noalloc(hipStream_t stream, const void* x, int x_dty
     set_error("dmh_ns_chain_noalloc: bad arguments (batch=%d rows=%d cols=%d)", batch, rows, cols);
     return DMH_EINVAL;
   }
-  const size_t need = chain_ws(nullptr, batch, chain_dims(rows, cols, orient_tall)).bytes;
+  const ChainDims d = chain_dims(rows, cols, orient_tall);
+  if (chain_check("dmh_ns_chain_noalloc", d)) return DMH_EINVAL;
+  const size_t need = chain_ws(nullptr, batch, d).bytes;
   if (need > (size_t)DMH_NS_SCRATCH_BYTES) {
     set_error("dmh_ns_chain_noalloc: batch=%d of %dx%d needs %zu bytes of workspace, more than "
               "the %zu-byte static scratch; use dmh_ns_chain with a caller workspace",

@@ -2435,7 +2435,9 @@ int dmh_deflated_polar_workspace_size(int batch, int n, int m, int r, size_t* by
     set_error("dmh_deflated_polar_workspace_size: null output");
     return DMH_EINVAL;
   }
-  if (check_dims("dmh_deflated_polar_workspace_size", batch, n, m, r)) return DMH_EINVAL;
+  if (check_dims("dmh_deflated_polar_workspace_size", batch, n, m, r) ||
+      chain_check("dmh_deflated_polar_workspace_size", chain_dims(n, m, 1)))
+    return DMH_EINVAL;
   *bytes = fused_bytes(batch, n, m, nullptr);
   return DMH_OK;
 }
@@ -2564,7 +2566,8 @@ int dmh_deflated_polar_front(hipStream_t stream, const float* A, const float* Om
   if (batch == 0) return DMH_OK;
   // ws stands in for the output pointer: the entry goes into the workspace
   if (clip_args("dmh_deflated_polar_front", A, Omega, ws, k, d, batch, n, m, r, kw, niter,
-                qr_passes, pad))
+                qr_passes, pad) ||
+      chain_check("dmh_deflated_polar_front", chain_dims(n, m, 1)))
     return DMH_EINVAL;
   size_t chain_off = 0;
   const size_t need = fused_bytes(batch, n, m, &chain_off);
@@ -2592,6 +2595,7 @@ int dmh_deflated_polar_chain(hipStream_t stream, int batch, int n, int m, const 
               m, steps);
     return DMH_EINVAL;
   }
+  if (chain_check("dmh_deflated_polar_chain", chain_dims(n, m, 1))) return DMH_EINVAL;
   size_t chain_off = 0;
   const size_t need = fused_bytes(batch, n, m, &chain_off);
   if (!ws || ws_bytes < need) {

@@ -382,7 +382,8 @@ class AdamwTable:
 
     @staticmethod
     def key_of(quads):
-        return tuple(t.data_ptr() for q in quads for t in q)
+        """Addresses of every tensor and each parameter's size, in table order."""
+        return tuple((t.data_ptr(), t.numel()) for q in quads for t in q)
 
 
 def adamw_step(tab, w1, w2, eps, decay, alpha):

@@ -339,19 +339,30 @@ class Muon(torch.optim.Optimizer):
         return True
 
     # -- the AdamW backup as one library launch per group (FUSED_GLUE) ----------
+    ADAMW_TABLES_KEPT = 4   # device tables kept per parameter group
     def _adamw_fused(self, group, params, lr, weight_decay, beta1, beta2, eps):
         """The AdamW loop below (muon.py:408-436) in one dmh_adamw_step launch per
         distinct step count: the same fp32 operations per element, the moments
         created and the step counts kept exactly as the loop does.  Returns False
-        (nothing done) when a tensor is not a contiguous fp32 GPU tensor."""
+        (nothing done) when a parameter, its gradient or an existing moment is not a
+        contiguous fp32 GPU tensor of the parameter's shape (the kernel indexes all
+        four flat).
+
+        The device table of a group's tensors is built once and reused while the
+        tensors stay at the same addresses: tables are cached per group by those
+        addresses (not by the step count, which only enters the scalar alpha), the
+        few most recent kept, so gradients that alternate between a couple of
+        buffers do not rebuild it either."""
         if not self.FUSED_GLUE:
             return False
         live = [p for p in params if p.grad is not None]
         if not live:
             return True
         for p in live:
+            st = self.state[p]
+            ts = [p.data, p.grad] + [st[k] for k in ("moment1", "moment2") if k in st]
             if any(not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous()
-                   for t in (p.data, p.grad)):
+                   or t.shape != p.shape for t in ts):
                 return False
         by_step = {}
         for p in live:
@@ -363,13 +374,15 @@ class Muon(torch.optim.Optimizer):
             state["step"] += 1
             by_step.setdefault(state["step"], []).append(
                 (p.data, p.grad, state["moment1"], state["moment2"]))
-        cache = self.__dict__.setdefault("_adamw_tables", {})
+        tables = self.__dict__.setdefault("_adamw_tables", {}).setdefault(id(group), {})
         for step, quads in by_step.items():
             key = _native.AdamwTable.key_of(quads)
-            tab = cache.get(id(group), {}).get(step)
-            if tab is None or tab.key != key:
+            tab = tables.pop(key, None)
+            if tab is None:
                 tab = _native.AdamwTable(quads)
-                cache[id(group)] = {step: tab}
+                while len(tables) >= self.ADAMW_TABLES_KEPT:
+                    tables.pop(next(iter(tables)))      # the least recently used
+            tables[key] = tab                           # most recently used last
             scale = (1 - beta1 ** step) / (1 - beta2 ** step) ** 0.5
             _native.adamw_step(tab, 1 - beta1, 1 - beta2, eps, 1 - lr * weight_decay,
                                -lr / scale)

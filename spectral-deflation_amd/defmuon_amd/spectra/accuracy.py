@@ -12,10 +12,11 @@ Polar-factor convergence (spectra/polar_convergence.py): for every matrix, the f
 methods with their production entries (polar_convergence.py:151-170) and the relative
 Frobenius error ||X_k - UV^T||_F / ||UV^T||_F against the fp64 polar factor after each
 of the 5 iterations (polar_convergence.py:173-188).  Entries and the deflation front-end
-run through this library; the iteration runs in bf16 through the library's chain (one
-launch per iteration, the training precision) or, with iter_dtype fp32, in fp32 torch
-matmuls on the GPU (the reference's default, which isolates estimation and mapping
-effects from bf16 rounding).  Rows: tag, step, matrix, method, rel_err_k0..k5,
+run through this library, and so does the iteration: `_horner_iterate` one step at a
+time in the study's dtype, as the reference's `run` does (polar_convergence.py:177-185),
+i.e. the library's bf16 MFMA chain (the training precision) or, with iter_dtype fp32
+(the reference's default, which isolates estimation and mapping effects from bf16
+rounding), its fp32 chain.  Rows: tag, step, matrix, method, rel_err_k0..k5,
 k_deflated, iter_dtype (polar_convergence.py:309-320).
 """
 
@@ -33,6 +34,7 @@ NS_ABC = (3.4445, -4.7750, 2.0315)
 NS_STEPS = 5
 SEED = 20260915                 # sketch seed base (polar_convergence.py:84)
 METHODS = ["ns5", "polarexpress", "deflated_ns", "deflated_pe"]
+ITER_DTYPES = {"bf16": torch.bfloat16, "fp32": torch.float32}
 
 
 def sketch_seed(step, lbl):
@@ -119,13 +121,6 @@ def schedule(method):
     return [NS_ABC] * NS_STEPS
 
 
-def _step_fp32(X, coef):
-    """One tall-convention step in fp32: X <- aX + X(bG + cG^2), G = X^T X."""
-    a, b, c = coef
-    G = X.mT @ X
-    return a * X + X @ (b * G + c * (G @ G))
-
-
 def rel_err(X, P):
     return float((X.double() - P).norm() / P.norm())
 
@@ -134,10 +129,10 @@ def run(method, A, P, seed, iter_dtype="bf16"):
     """(rel_err after k = 0..NS_STEPS iterations, deflation width) for one method on
     the tall matrix A with exact polar factor P (polar_convergence.py:178-188)."""
     X0, k = entry(method, A, seed)
-    X = X0.to(torch.bfloat16 if iter_dtype == "bf16" else torch.float32)
+    X = X0.to(ITER_DTYPES[iter_dtype])
     rel = [rel_err(X, P)]
     for coef in schedule(method):
-        X = DB._horner_iterate(X, [coef]) if iter_dtype == "bf16" else _step_fp32(X, coef)
+        X = DB._horner_iterate(X, [coef])
         rel.append(rel_err(X, P))
     return rel, k
 

@@ -78,3 +78,31 @@ def test_workspace_sizes_for_empty_batch(lib):
                "dmh_deflated_polar_workspace_size"):
         assert getattr(lib, fn)(0, 512, 256, 14, ctypes.byref(n)) == 0, fn
     assert lib.dmh_ns_workspace_size(0, 512, 256, 1, ctypes.byref(n)) == 0
+
+
+def test_chain_refuses_operands_beyond_32bit_addressing(lib):
+    """The bf16 chain addresses each padded operand through 32-bit buffer descriptors
+    and offsets: a matrix whose padded bf16 iterate reaches 2^31 bytes is refused with
+    status 1 by every entry that runs the chain, before any HIP call; one just below
+    the limit is accepted."""
+    n = ctypes.c_size_t()
+    v, dummy = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    coeffs = (ctypes.c_double * 3)(3.4445, -4.7750, 2.0315)
+    big, ok = (32768, 32768), (32768, 32512)     # 2^31 and 2^31 - 2^24 bytes of bf16
+    assert lib.dmh_ns_workspace_size(1, *ok, 1, ctypes.byref(n)) == 0
+    assert lib.dmh_ns_workspace_size(1, *big, 1, ctypes.byref(n)) == 1
+    assert b"32-bit" in lib.dmh_last_error()
+    assert lib.dmh_ns_chain(v, dummy, 1, 1, *big, 1 << 30, big[1], 1, dummy, 1, 0, coeffs, 1,
+                            dummy, 16) == 1
+    assert b"32-bit" in lib.dmh_last_error()
+    assert lib.dmh_ns_chain_noalloc(v, dummy, 1, 1, *big, 1 << 30, big[1], 1, dummy, 1, 0,
+                                    coeffs, 1) == 1
+    assert b"32-bit" in lib.dmh_last_error()
+    assert lib.dmh_deflated_polar_workspace_size(1, *ok, 64, ctypes.byref(n)) == 0
+    assert lib.dmh_deflated_polar_workspace_size(1, *big, 64, ctypes.byref(n)) == 1
+    assert b"32-bit" in lib.dmh_last_error()
+    assert lib.dmh_deflated_polar_chain(v, 1, *big, coeffs, 1, dummy, dummy, 16) == 1
+    assert b"32-bit" in lib.dmh_last_error()
+    assert lib.dmh_deflated_polar_front(v, dummy, dummy, 1, *big, 64, 32, 0.1, 0.1, 1.01, 1,
+                                        1, dummy, dummy, dummy, 16) == 1
+    assert b"32-bit" in lib.dmh_last_error()

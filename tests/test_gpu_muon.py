@@ -308,3 +308,76 @@ def test_fused_adamw_equals_torch_ops(muon_mod, betas):
         assert torch.equal(m0[k][0], m1[k][0]), ("moment1", k)
         assert torch.equal(m0[k][1], m1[k][1]), ("moment2", k)
         assert torch.equal(p0[k], p1[k]), ("param", k, (p0[k] - p1[k]).abs().max().item())
+
+
+def test_fused_adamw_reuses_its_table(muon_mod, monkeypatch):
+    """The fused AdamW's device table is built on the first step and reused while the
+    tensors stay put: steps 2 and 3 build no AdamwTable (the same object, the same
+    device memory), and the parameters and moments stay bit for bit where the
+    reference's per-parameter loop (muon.py:408-436) leaves them.  Gradients are
+    written in place, so they keep their addresses as a training loop's do."""
+    muon, _ = muon_mod
+    from defmuon_amd import _native
+    built = []
+    base_init = _native.AdamwTable.__init__
+
+    def counting_init(self, quads):
+        built.append(len(quads))
+        base_init(self, quads)
+
+    monkeypatch.setattr(_native.AdamwTable, "__init__", counting_init)
+    shapes = {"wte.weight": (257, 31), "wpe.weight": (33, 7), "h.0.ln_1.bias": (4099,)}
+    results = {}
+    for fused in (False, True):
+        g = torch.Generator().manual_seed(5)
+        params = {k: torch.nn.Parameter((torch.randn(*v, generator=g) * 0.02).to(DEV))
+                  for k, v in shapes.items()}
+        grads = {k: (torch.randn(*v, generator=g) * 1e-2).to(DEV) for k, v in shapes.items()}
+        for k, p in params.items():
+            p.grad = torch.empty_like(p)
+        opt = muon.Muon(list(params.items()), lr=0.02, weight_decay=0.1, momentum=0.9,
+                        adamw_betas=(0.9, 0.95), adamw_eps=1e-8, ns_steps=5,
+                        polar_method="ns5")
+        opt.FUSED_GLUE = fused
+        built.clear()
+        seen = []
+        for step in range(3):
+            for k, p in params.items():
+                p.grad.copy_(grads[k] * (1.0 + 0.5 * step) - 0.003 * step)
+            opt.step()
+            if fused:
+                tabs = list(opt._adamw_tables[id(opt.param_groups[0])].values())
+                assert len(tabs) == 1, step
+                seen.append((tabs[0], tabs[0].table.data_ptr(), tabs[0].chunks.data_ptr()))
+        torch.cuda.synchronize()
+        if fused:
+            assert built == [len(shapes)], built          # one table, built on step 1
+            assert all(s[0] is seen[0][0] and s[1:] == seen[0][1:] for s in seen), seen
+        else:
+            assert built == []
+        results[fused] = ({k: v.detach().clone() for k, v in params.items()},
+                          {k: (opt.state[p]["moment1"].clone(), opt.state[p]["moment2"].clone())
+                           for k, p in params.items()})
+    (p0, m0), (p1, m1) = results[False], results[True]
+    for k in shapes:
+        assert torch.equal(m0[k][0], m1[k][0]) and torch.equal(m0[k][1], m1[k][1]), k
+        assert torch.equal(p0[k], p1[k]), k
+
+
+def test_fused_adamw_declines_foreign_moments(muon_mod):
+    """Moments the fused kernel cannot index flat (here a non-contiguous moment, as a
+    fallback loop or load_state_dict could leave) send the group to the torch loop,
+    whose result the fused path would otherwise have to match."""
+    muon, _ = muon_mod
+    g = torch.Generator().manual_seed(6)
+    p = torch.nn.Parameter((torch.randn(24, 16, generator=g) * 0.02).to(DEV))
+    opt = muon.Muon([("wte.weight", p)], lr=0.02, weight_decay=0.1, momentum=0.9,
+                    adamw_betas=(0.9, 0.95), adamw_eps=1e-8, ns_steps=5, polar_method="ns5")
+    p.grad = (torch.randn(24, 16, generator=g) * 1e-2).to(DEV)
+    st = opt.state[p]
+    st["step"] = 1
+    st["moment1"] = torch.zeros(16, 24, device=DEV).mT          # non-contiguous view
+    st["moment2"] = torch.zeros(24, 16, device=DEV)
+    group = opt.param_groups[0]
+    assert not opt._adamw_fused(group, [p], 0.02, 0.1, 0.9, 0.95, 1e-8)
+    assert st["step"] == 1                                       # nothing was touched
