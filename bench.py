@@ -103,11 +103,14 @@ def make_inputs(groups, device, seed=1234, kind="spiked"):
     return out
 
 
-def polar_step(fac, stacks, bd_step, ns_steps, events=None):
+def polar_step(fac, stacks, bd_step, ns_steps, events=None, ns_timing="sequential"):
     """One polar step over all groups, as the optimizer runs it
     (_DeflatedPolarBase.polar_groups: the groups' clips, then their iterations);
     returns per-group (U, k).  With `events`, appends a list of (start, end) HIP
-    event pairs recorded on the launch stream around each group's NS chain."""
+    event pairs recorded on the launch stream: ns_timing "sequential", one pair
+    around each group's NS chain, the chains one after the other once every
+    front-end has finished; "concurrent", one pair around the chain phase, every
+    group's chain on its own stream once every front-end has finished."""
     import torch
     from defmuon_amd.optim import deflation_batched as DB
     gens = []
@@ -115,11 +118,14 @@ def polar_step(fac, stacks, bd_step, ns_steps, events=None):
         gen = torch.Generator(device=A.device)
         gen.manual_seed((bd_step * 1009 + gi * 9176867) % (2 ** 62))
         gens.append(gen)
-    evs = None
-    if events is not None:
+    evs = window = None
+    if events is not None and ns_timing == "concurrent" and len(stacks) > 1:
+        window = tuple(torch.cuda.Event(enable_timing=True) for _ in range(2))
+        events.append([window])
+    elif events is not None:
         evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in stacks]
         events.append(evs)
-    res = fac.polar_groups(stacks, gens, steps=ns_steps, chain_events=evs)
+    res = fac.polar_groups(stacks, gens, steps=ns_steps, chain_events=evs, chain_window=window)
     outs = []
     for A, (U, kvec, _) in zip(stacks, res):
         if DB._GATE_ACC[0] is None:
@@ -149,22 +155,20 @@ def make_plain_inputs(pgroups, device, seed=4321, gaussian=False):
 
 def plain_step(arm, stacks, pgroups, ns_steps, events=None):
     """One plain-arm polar step (muon.py:361-386 factorizer calls over every Muon
-    parameter) with one launch per group, as Muon._muon_step_plain_grouped runs it."""
+    parameter) with one launch per group, the groups on side streams of their own, as
+    Muon._muon_step_plain_grouped runs it (plain_group_chains)."""
     import torch
     from defmuon_amd import _native
     from defmuon_amd.optim.muon import NS_ABC
     from defmuon_amd.optim.polar_express import pe_schedule
+    from defmuon_amd.optim.muon import plain_group_chains
     mode, sched = (1, [NS_ABC] * ns_steps) if arm == "ns5" else (2, pe_schedule(ns_steps))
-    evs = []
-    outs = []
-    for X, (_, _, _, tall) in zip(stacks, pgroups):
-        ev = tuple(torch.cuda.Event(enable_timing=True) for _ in range(2))
-        ev[0].record()
-        outs.append(_native.ns_chain(X, tall, mode, sched))
-        ev[1].record()
-        evs.append(ev)
+    ev = tuple(torch.cuda.Event(enable_timing=True) for _ in range(2))
+    ev[0].record()
+    outs = plain_group_chains(stacks, [tall for _, _, _, tall in pgroups], mode, sched)
+    ev[1].record()
     if events is not None:
-        events.append(evs)
+        events.append([ev])
     return outs
 
 
@@ -596,6 +600,10 @@ def main():
     ap.add_argument("--arm", default="deflated_ns_cut",
                     choices=["deflated_ns_cut", "deflated_pe_cut", "ns5", "polarexpress"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ns-timing", default="sequential", choices=["sequential", "concurrent"],
+                    help="the deflated arms' NS-chain pass: the groups' chains one after the "
+                         "other (sequential) or together, each on its group's stream "
+                         "(concurrent), once every front-end has finished")
     ap.add_argument("--inputs", default="spiked", choices=["spiked", "spiked-cpu", "gaussian"],
                     help="synthetic momenta: spiked spectra generated on the GPU (default), "
                          "the same generated on the host (counter runs: no GPU solver "
@@ -681,7 +689,7 @@ def main():
         stacks = make_inputs(groups, dev, kind=args.inputs)
 
         def step(i, events=None):
-            return polar_step(fac, stacks, i, 5, events)
+            return polar_step(fac, stacks, i, 5, events, args.ns_timing)
     torch.cuda.synchronize()
 
     log(f"bench: warmup {args.warmup}")
@@ -719,6 +727,14 @@ def main():
         seq1.record()
         torch.cuda.synchronize()
         seq_ms = seq0.elapsed_time(seq1) / args.steps
+        # the other NS-chain timing, reported beside the primary one
+        other = "concurrent" if args.ns_timing == "sequential" else "sequential"
+        log(f"bench: NS-chain pass ({other} chains), {args.steps} steps")
+        events2 = []
+        for s in range(args.steps):
+            polar_step(fac, stacks, args.warmup + s + 1, 5, events2, other)
+        torch.cuda.synchronize()
+        ns_ms_other = sum(e0.elapsed_time(e1) for evs in events2 for e0, e1 in evs) / args.steps
     ns_ms = sum(e0.elapsed_time(e1) for evs in events for e0, e1 in evs) / args.steps
     # plain arms: the chain is the whole step; deflated arms: the front-ends (with the
     # chains of the sequential pass subtracted) and the gate ticks
@@ -781,11 +797,22 @@ def main():
                      "kernel": "NS chain (gemm_nt_bf16 K1/K2/K3 launches of a polar step), "
                                "canonical dense 4m^2n+2m^3 FLOP per matrix-iteration",
                      "flops_per_step": flops, "ns_ms_per_step": ns_ms,
-                     "ns_timing": "HIP events around each chain call on the launch stream"
-                                  + ("" if plain else ", in a pass of the same steps with "
-                                     "the chains one after the other (the timed steps "
-                                     "overlap them with the other group's work)")},
+                     "ns_timing": ("HIP events on the launch stream around the plain "
+                                   "arm's group chains (entry normalisation included; the "
+                                   "groups on side streams of their own, as the optimizer "
+                                   "runs them)") if plain else
+                                  ("HIP events on the launch stream, in a pass of the same "
+                                   "steps once both front-ends have finished (the timed "
+                                   "steps overlap the chains with the other group's work): "
+                                   + ("one pair around each group's chain, the chains one "
+                                      "after the other" if args.ns_timing == "sequential" else
+                                      "one pair around the chain phase, every group's chain "
+                                      "on its own stream"))},
         "frontend_ms_per_step": None if plain else front_ms,
+        "ns_other_timing": None if plain else {
+            "ns_timing": other, "ns_ms_per_step": ns_ms_other,
+            "achieved": flops / (ns_ms_other * 1e-3) / 1e12,
+            "frac": flops / (ns_ms_other * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
         "gate": None if plain else st,
         "cpu_baseline": cpu,
     }

@@ -34,6 +34,7 @@
 #include "ns_chain.h"
 
 #include <mutex>
+#include <stdlib.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -69,31 +70,46 @@ void set_error(const char* fmt, ...) {
 // banks.  The swizzle is applied by choosing, for each lane, which global chunk it
 // fetches into its fixed LDS slot.
 // ---------------------------------------------------------------------------
-constexpr int TILE = CHAIN_TILE;
 constexpr int TK = 64;
 constexpr int NSTAGE = 2;
 constexpr int KSUB = TK / 16;                // k16 MFMA substeps per stage
 constexpr int CHUNKS = TK / 8;               // 16-byte chunks per LDS row
 constexpr int ROWB = TK * 2;                 // bytes per LDS row
-constexpr int OPB = TILE * ROWB;             // bytes per operand tile (32 KB)
-constexpr int STAGEB = 2 * OPB;              // P + Q
+constexpr int LROWS = 64 / CHUNKS;           // tile rows per load instruction
 static_assert(KSUB == 4 && CHUNKS == 8, "the main loop is written for 64-wide K stages");
-// 8 waves, two per SIMD (so one wave's MFMAs fill the other's waits), as a
-// 2 x 4 grid of 128 x 64 wave tiles: 4 x 2 MFMA blocks of 32 x 32 per wave.
-constexpr int GEMM_WAVES = 8;
-constexpr int GEMM_THREADS = 64 * GEMM_WAVES;
-constexpr int WAVES_N = 4;                      // waves along the Q rows (output columns)
-constexpr int WT_M = TILE / (GEMM_WAVES / WAVES_N), WT_N = TILE / WAVES_N;
-constexpr int BM = WT_M / 32, BN = WT_N / 32;   // MFMA blocks per wave
-constexpr int LROWS = 64 / CHUNKS;                // tile rows per load instruction
-constexpr int LQ = TILE / GEMM_WAVES / LROWS;   // loads per operand per stage per lane
 static_assert(NSTAGE == 2, "the ring waits are written for two slots (vmcnt(0))");
-constexpr int RING_BYTES = NSTAGE * STAGEB;
-// epilogue staging: one 32 x 64 bf16 block row of the wave's output at a time
-constexpr int EPI_WAVE_BYTES = 32 * WT_N * 2;
-static_assert(WT_N == 64, "the epilogue staging is written for 64-column wave tiles");
-constexpr int SMEM_BYTES = RING_BYTES + GEMM_WAVES * EPI_WAVE_BYTES;
-static_assert(SMEM_BYTES <= 160 * 1024, "LDS ring and epilogue staging must fit the 160 KB of a CU");
+
+// Output tile shapes.  TL = 256: 8 waves (two per SIMD, so one wave's MFMAs fill the
+// other's waits) as a 2 x 4 grid of 128 x 64 wave tiles (4 x 2 MFMA blocks of 32 x 32
+// per wave), one workgroup per CU.  TL = 128, for matrices too small to give every
+// CU several 256 x 256 tiles: 4 waves as a 2 x 2 grid of 64 x 64 wave tiles (2 x 2
+// blocks), 80 KB of LDS, two workgroups (again two waves per SIMD) per CU.
+template <int TL>
+struct GemmCfg {
+  static constexpr int TILE = TL;
+  static constexpr int WAVES = TL == 256 ? 8 : 4;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int WAVES_N = TL == 256 ? 4 : 2;   // waves along the Q rows (output columns)
+  static constexpr int WT_M = TILE / (WAVES / WAVES_N), WT_N = TILE / WAVES_N;
+  static constexpr int BM = WT_M / 32, BN = WT_N / 32;   // MFMA blocks per wave
+  static constexpr int OPB = TILE * ROWB;               // bytes per operand tile
+  static constexpr int STAGEB = 2 * OPB;                // P + Q
+  static constexpr int LQ = TILE / WAVES / LROWS;       // loads per operand per stage per lane
+  static constexpr int KROWB = TILE * 2;                // bytes per K-major LDS row
+  static constexpr int KCH = TILE / 8;                  // 16-byte chunks per K-major row
+  static constexpr int RING_BYTES = NSTAGE * STAGEB;
+  // epilogue staging: one 32 x 64 bf16 block row of the wave's output at a time
+  static constexpr int EPI_WAVE_BYTES = 32 * WT_N * 2;
+  static constexpr int SMEM_BYTES = RING_BYTES + WAVES * EPI_WAVE_BYTES;
+  static constexpr int WG_PER_CU = (160 * 1024) / SMEM_BYTES;
+  // vector memory instructions a wave's epilogue issues for a whole, aligned wave tile
+  static constexpr int ROW_STORES = 4 * BM, T_STORES = 2 * BM * BN, AUX_LOADS = 4 * BM;
+  static_assert(WT_N == 64, "the epilogue staging is written for 64-column wave tiles");
+  static_assert(BM % 2 == 0, "the transposed epilogue pass takes block rows in pairs");
+  static_assert(LQ == 4 && TK / WAVES * KROWB == LQ * 1024, "loader layout");
+  static_assert(SMEM_BYTES <= 160 * 1024, "LDS ring and epilogue staging must fit 160 KB");
+  static_assert(WAVES * WG_PER_CU == 8, "two waves per SIMD");
+};
 
 enum { EPI_STORE = 0, EPI_POLY = 1 };
 
@@ -178,7 +194,7 @@ __device__ __forceinline__ void ring_barrier() {
 // covers the later stages, R * 128 bytes apart.  K-major layout (TNL = 1): columns
 // t*TILE..+TILE-1 of a matrix whose row k holds the operand's values for
 // contraction index k (R = K rows): 4 whole block columns, R * 128 bytes each.
-template <int TNL>
+template <int TNL, int TILE>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16* base, long long bs,
                                                            int R, int K, int b, int t) {
   if (TNL) {
@@ -198,12 +214,24 @@ typedef __attribute__((address_space(3))) s16x4* lds_s16x4_t;
 // 16 lanes, result lane j, element e is element j % 4 of the 8-byte chunk addressed
 // by lane 4 e + j / 4.  Lane 16 g + 4 e + q addresses row k0 + e, columns c0 + 4 q
 // .. +3, so lane 16 g + j receives column c0 + j at rows k0 .. k0+3; the second read
-// (rows k0+4 .. k0+7) is 4 rows = 2048 bytes further.
-__device__ __forceinline__ bf16x8 lds_tr_frag(const char* p) {
+// (rows k0+4 .. k0+7) is 4 rows (of krowb bytes) further.
+__device__ __forceinline__ bf16x8 lds_tr_frag(const char* p, int krowb) {
   const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(p));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(p + 4 * 512));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t)(p + 4 * krowb));
   const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), h4 = __builtin_bit_cast(bf16x4, hi);
   return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// The GEMM's builtins behind plain device functions: inside the kernel template their
+// arguments have types that depend on the tile size, and the host pass of the
+// compiler rejects a target builtin whose call it has to resolve at instantiation.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, char* lds, int voff,
+                                           int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_32x32x16(const bf16x8& a, const bf16x8& b,
+                                                 const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // Store 8 consecutive bf16 at dst (elements q with mask bit q set); a full, aligned
@@ -223,11 +251,16 @@ __device__ __forceinline__ void store8(bf16* dst, const bf16x8& v, unsigned mask
 // TNL = 0: C[i][j] = sum_k P[i][k] Q[j][k] (both operands K-contiguous rows).
 // TNL = 1: C[i][j] = sum_k P[k][i] Q[k][j] (both operands K-major: their row k holds
 //          the values of every output index for contraction index k).
-template <int EPI, int TNL>
-__global__ __attribute__((amdgpu_flat_work_group_size(GEMM_THREADS, GEMM_THREADS),
-                          amdgpu_waves_per_eu(GEMM_WAVES / 4, GEMM_WAVES / 4)))
+template <int EPI, int TNL, int TL>
+__global__ __attribute__((amdgpu_flat_work_group_size(GemmCfg<TL>::THREADS, GemmCfg<TL>::THREADS),
+                          amdgpu_waves_per_eu(2, 2)))
 void gemm_nt_bf16(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char smem[SMEM_BYTES];
+  using C = GemmCfg<TL>;
+  constexpr int TILE = C::TILE, GEMM_WAVES = C::WAVES, WAVES_N = C::WAVES_N;
+  constexpr int WT_M = C::WT_M, WT_N = C::WT_N, BM = C::BM, BN = C::BN;
+  constexpr int OPB = C::OPB, STAGEB = C::STAGEB, LQ = C::LQ, KROWB = C::KROWB, KCH = C::KCH;
+  constexpr int RING_BYTES = C::RING_BYTES, EPI_WAVE_BYTES = C::EPI_WAVE_BYTES;
+  __shared__ __attribute__((aligned(1024))) char smem[C::SMEM_BYTES];
 
   int lid, lstep, lend;
   tile_range(g.total_tiles, lid, lstep, lend);
@@ -246,22 +279,23 @@ void gemm_nt_bf16(GemmArgs g) {
   // scalar offset) and the LDS destination (M0) is wave-uniform, so a load costs no
   // VALU work.
   //
-  // K-major tiles (TNL) are 64 rows (k) of 512 B (32 chunks of 16 B, the 256 output
-  // indices); chunk c of row r sits in slot c ^ 4 (r & 3), which spreads the
-  // transposing fragment reads (4 rows x 4 chunks per 16 lanes) over every bank.
-  // Instruction q of wave w fills rows 8 w + 2 q and 8 w + 2 q + 1 (1 KB), so the
-  // LDS destinations are the same as for the row-operand tiles.
+  // K-major tiles (TNL) are 64 rows (k) of KROWB = 2 TILE bytes (KCH chunks of 16 B,
+  // the TILE output indices); chunk c of row r sits in slot c ^ 4 (r & 3), which
+  // spreads the transposing fragment reads (4 rows x 4 chunks per 16 lanes) over the
+  // banks.  Instruction q of wave w fills the 1024 / KROWB rows starting at
+  // (64 / GEMM_WAVES) w + (1024 / KROWB) q (1 KB), so the LDS destinations are the
+  // same as for the row-operand tiles.
   // In global memory (block layout): a row-operand stage is 256 rows of 128 B, one
   // after the other, and the next stage is R * 128 bytes further; a K-major stage is
   // 64 rows of four 128-byte pieces, one per block column (R * 128 bytes apart), and
   // the next stage is the next 8 KB block of each column.
   int boffP[LQ], boffQ[LQ];   // byte offsets within the tile
   if (TNL) {
-    static_assert(TK / GEMM_WAVES == 2 * LQ && TILE * 2 == 32 * 16, "K-major loader layout");
+    constexpr int RPI = 1024 / KROWB;   // K-major rows per load instruction
 #pragma unroll
     for (int q = 0; q < LQ; ++q) {
-      const int r = (TK / GEMM_WAVES) * wave + 2 * q + (lane >> 5);
-      const int c = (lane & 31) ^ (4 * (r & 3));
+      const int r = (TK / GEMM_WAVES) * wave + RPI * q + lane / KCH;
+      const int c = (lane % KCH) ^ (4 * (r & 3));
       boffP[q] = (c >> 3) * g.p_rows * ROWB + r * ROWB + (c & 7) * 16;
       boffQ[q] = (c >> 3) * g.q_rows * ROWB + r * ROWB + (c & 7) * 16;
     }
@@ -287,10 +321,8 @@ void gemm_nt_bf16(GemmArgs g) {
     char* dQ = dP + OPB;                                                               \
     const int soP = (k0) * kstepP, soQ = (k0) * kstepQ;                                \
     _Pragma("unroll") for (int q = 0; q < LQ; ++q) {                                   \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_ptr_t)(dP + q * LROWS * ROWB), 16, \
-                                               boffP[q], soP, 0, 0);                   \
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr_t)(dQ + q * LROWS * ROWB), 16, \
-                                               boffQ[q], soQ, 0, 0);                   \
+      load_lds16(rp, dP + q * LROWS * ROWB, boffP[q], soP);                            \
+      load_lds16(rq, dQ + q * LROWS * ROWB, boffQ[q], soQ);                            \
     }                                                                                  \
   } while (0)
 
@@ -306,7 +338,7 @@ void gemm_nt_bf16(GemmArgs g) {
       const int gq = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
       const int k = 16 * st + 8 * (gq >> 1) + e;
       const int c = c0 + 16 * (gq & 1) + 4 * q;
-      return k * 512 + (((c >> 3) ^ (4 * (k & 3))) * 16) + (c & 7) * 2;
+      return k * KROWB + (((c >> 3) ^ (4 * (k & 3))) * 16) + (c & 7) * 2;
     }
     const int row = c0 + r32;
     return row * ROWB + ((2 * st + hi) ^ lds_swz(row)) * 16;
@@ -323,17 +355,17 @@ void gemm_nt_bf16(GemmArgs g) {
 #define DMH_RD(F, base, st)                                                            \
   do {                                                                                 \
     _Pragma("unroll") for (int i = 0; i < BM; ++i)                                     \
-      F##p[i] = TNL ? lds_tr_frag((base) + offP[i][st])                                \
+      F##p[i] = TNL ? lds_tr_frag((base) + offP[i][st], KROWB)                         \
                     : *(const bf16x8*)((base) + offP[i][st]);                          \
     _Pragma("unroll") for (int j = 0; j < BN; ++j)                                     \
-      F##q[j] = TNL ? lds_tr_frag((base) + offQ[j][st])                                \
+      F##q[j] = TNL ? lds_tr_frag((base) + offQ[j][st], KROWB)                         \
                     : *(const bf16x8*)((base) + offQ[j][st]);                          \
   } while (0)
 #define DMH_MM(F)                                                                      \
   do {                                                                                 \
     _Pragma("unroll") for (int i = 0; i < BM; ++i)                                     \
       _Pragma("unroll") for (int j = 0; j < BN; ++j)                                   \
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F##q[j], F##p[i], acc[i][j], 0, 0, 0); \
+        acc[i][j] = mfma_32x32x16(F##q[j], F##p[i], acc[i][j]);                       \
   } while (0)
   // MFMAs of one substep with the next substep's fragment reads among them
 #define DMH_SCHED_SUB()                                                                \
@@ -342,14 +374,15 @@ void gemm_nt_bf16(GemmArgs g) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                               \
       __builtin_amdgcn_sched_group_barrier(0x100, TNL ? 2 : 1, 0);                     \
     }                                                                                  \
-    __builtin_amdgcn_sched_group_barrier(0x008, BM * BN - (BM + BN), 0);               \
+    if constexpr (BM * BN > BM + BN)                                                   \
+      __builtin_amdgcn_sched_group_barrier(0x008, BM * BN - (BM + BN), 0);             \
   } while (0)
 
   const int nk = g.K / TK;
   int b, ti, tj;
   decode_tile(g, lid, b, ti, tj);
-  __amdgpu_buffer_rsrc_t rP = tile_rsrc<TNL>(g.P, g.p_bs, g.p_rows, g.K, b, ti);
-  __amdgpu_buffer_rsrc_t rQ = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_rows, g.K, b, tj);
+  __amdgpu_buffer_rsrc_t rP = tile_rsrc<TNL, TILE>(g.P, g.p_bs, g.p_rows, g.K, b, ti);
+  __amdgpu_buffer_rsrc_t rQ = tile_rsrc<TNL, TILE>(g.Q, g.q_bs, g.q_rows, g.K, b, tj);
   // Each tile walks its K stages starting at stage kspread (ti + tj) % nk and
   // wrapping around: the tiles that share an operand panel (same ti, or same tj) are
   // then at different K stages at any moment, so each line of a shared panel is
@@ -372,8 +405,8 @@ void gemm_nt_bf16(GemmArgs g) {
     const bool more = nlid < lend;
     int nb = b, nti = ti, ntj = tj;
     if (more) decode_tile(g, nlid, nb, nti, ntj);
-    const __amdgpu_buffer_rsrc_t rPn = tile_rsrc<TNL>(g.P, g.p_bs, g.p_rows, g.K, nb, nti);
-    const __amdgpu_buffer_rsrc_t rQn = tile_rsrc<TNL>(g.Q, g.q_bs, g.q_rows, g.K, nb, ntj);
+    const __amdgpu_buffer_rsrc_t rPn = tile_rsrc<TNL, TILE>(g.P, g.p_bs, g.p_rows, g.K, nb, nti);
+    const __amdgpu_buffer_rsrc_t rQn = tile_rsrc<TNL, TILE>(g.Q, g.q_bs, g.q_rows, g.K, nb, ntj);
 
     // Main loop of one tile, software-pipelined at two levels:
     //  * LDS ring: stage kt+1 is in flight while stage kt is consumed;
@@ -390,7 +423,9 @@ void gemm_nt_bf16(GemmArgs g) {
     // (the builtin, not inline asm, so that the compiler's own wait tracking sees it;
     // encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left at their maxima)
     switch (vm_after) {
+      case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
       case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
+      case 24: __builtin_amdgcn_s_waitcnt(0x4F78); break;
       case 32: __builtin_amdgcn_s_waitcnt(0x8F70); break;
       case 48: __builtin_amdgcn_s_waitcnt(0xCF70); break;
       default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
@@ -508,7 +543,9 @@ void gemm_nt_bf16(GemmArgs g) {
       // aligned: the epilogue then issues a known number of memory instructions
       const bool whole = wi0 + WT_M <= g.valid_i && wj0 + WT_N <= g.valid_j &&
                          (!outb || al_out) && (!outtb || al_outT);
-      vm_after = whole ? (outb ? 16 : 0) + (outtb ? 16 : 0) + (EPI == EPI_POLY ? 16 : 0) : -1;
+      vm_after = whole ? (outb ? C::ROW_STORES : 0) + (outtb ? C::T_STORES : 0) +
+                             (EPI == EPI_POLY ? C::AUX_LOADS : 0)
+                       : -1;
       // POLY: the aux of block row 0 is requested up front and that of row bi+1 once
       // row bi's accumulators are staged, so the reads run one block row ahead of
       // their use (latency hidden under the staging, registers bounded)
@@ -834,8 +871,8 @@ ChainDims chain_dims(int rows, int cols, int orient_tall) {
   ChainDims d;
   d.n = orient_tall ? rows : cols;
   d.m = orient_tall ? cols : rows;
-  d.np = ceil_div(d.n, TILE) * TILE;
-  d.mp = ceil_div(d.m, TILE) * TILE;
+  d.np = ceil_div(d.n, CHAIN_TILE) * CHAIN_TILE;
+  d.mp = ceil_div(d.m, CHAIN_TILE) * CHAIN_TILE;
   return d;
 }
 
@@ -880,22 +917,55 @@ static int device_cus() {
   return cus[dev];
 }
 
-template <int EPI, int TNL>
-static int launch_gemm(GemmArgs g, int batch, hipStream_t stream, const char* what) {
+// One persistent launch of a GEMM phase with TILE x TILE output tiles over rows x cols
+// outputs per matrix (multiples of 256); one workgroup per free workgroup slot
+// (GemmCfg::WG_PER_CU per compute unit), or fewer when there are fewer tiles.
+template <int EPI, int TNL, int TL>
+static int launch_gemm_tl(GemmArgs g, int rows, int cols, int batch, hipStream_t stream,
+                          const char* what) {
+  using Cf = GemmCfg<TL>;
+  g.tiles_m = rows / TL;
+  g.tiles_n = cols / TL;
   const long long per = g.sym ? (long long)g.tiles_m * (g.tiles_m + 1) / 2
                               : (long long)g.tiles_m * g.tiles_n;
   const long long tiles = per * batch;
-  const int cus = device_cus();
-  if (tiles <= 0 || tiles > 0x7fffffffLL || cus <= 0) {
-    set_error("%s: bad grid (%lld tiles, %d compute units)", what, tiles, cus);
+  const long long slots = (long long)device_cus() * Cf::WG_PER_CU;
+  if (tiles <= 0 || tiles > 0x7fffffffLL || slots <= 0) {
+    set_error("%s: bad grid (%lld tiles, %lld workgroup slots)", what, tiles, slots);
     return DMH_EINVAL;
   }
   g.total_tiles = (int)tiles;
   g.batch = batch;
-  const int grid = (int)(tiles < cus ? tiles : cus);
-  hipLaunchKernelGGL((gemm_nt_bf16<EPI, TNL>), dim3(grid), dim3(GEMM_THREADS), 0, stream, g);
+  const int grid = (int)(tiles < slots ? tiles : slots);
+  hipLaunchKernelGGL((gemm_nt_bf16<EPI, TNL, TL>), dim3(grid), dim3(Cf::THREADS), 0, stream, g);
   DMH_CHECK_LAUNCH(what);
   return DMH_OK;
+}
+
+template <int EPI, int TNL>
+static int launch_gemm(const GemmArgs& g, int tile, int rows, int cols, int batch,
+                       hipStream_t stream, const char* what) {
+  return tile == 128 ? launch_gemm_tl<EPI, TNL, 128>(g, rows, cols, batch, stream, what)
+                     : launch_gemm_tl<EPI, TNL, 256>(g, rows, cols, batch, stream, what);
+}
+
+// Output tile size of the three phases (K1, K2, K3) for a shape.  Chosen from the
+// shape alone, never from the batch, so a matrix's result does not depend on the
+// batch it is computed in (the tile fixes each output's K-walk order).  The m x m
+// products of a matrix with m <= 768 have at most 6 upper 256 x 256 tiles, too few to
+// keep the CUs busy: they run on 128 x 128 tiles (GPT-2 small, m = 768: the chain
+// 1.91 -> 1.59 ms per deflated polar step); the tall product T B' keeps 256 x 256
+// tiles there (128 x 128: 1.66 ms), as do K1 and K2 from m = 1024 on (GPT-2 medium
+// 6.10 ms with 256 x 256 tiles everywhere, 6.31 with 128 x 128 for K1).
+static void phase_tiles(const ChainDims& d, int tile[3]) {
+  const int small = d.mp <= 768 ? 128 : 256;
+  tile[0] = small;
+  tile[1] = small;
+  tile[2] = 256;
+  const char* env = getenv("DMH_CHAIN_TILES");   // tuning override "k1,k2,k3"
+  int t[3];
+  if (env && sscanf(env, "%d,%d,%d", &t[0], &t[1], &t[2]) == 3)
+    for (int i = 0; i < 3; ++i) tile[i] = t[i] == 128 ? 128 : 256;
 }
 
 int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const ChainDims& d,
@@ -908,7 +978,8 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     DMH_CHECK_LAUNCH("copy_out");
     return DMH_OK;
   }
-  const int tm = d.mp / TILE, tn = d.np / TILE;
+  int tl[3];
+  phase_tiles(d, tl);
   // Consecutive launches walk the batch in opposite directions, so each one starts
   // on the matrices the previous one wrote last, which are still in the memory-side
   // cache (the group's operands are several times its size).  The entry pack wrote
@@ -927,13 +998,14 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     GemmArgs g1{};
     g1.P = Tc; g1.p_bs = (long long)d.np * d.mp; g1.p_rows = d.np;
     g1.Q = Tc; g1.q_bs = g1.p_bs; g1.q_rows = d.np;
-    g1.K = d.np; g1.tiles_m = tm; g1.tiles_n = tm; g1.sym = 1;
+    g1.K = d.np; g1.sym = 1;
     g1.out = Am; g1.out_bs = (long long)d.mp * d.mp; g1.out_rows = d.mp;
     g1.outT = Am; g1.outT_bs = g1.out_bs; g1.outT_rows = d.mp;
     g1.valid_i = d.mp; g1.valid_j = d.mp;
     g1.rev = rev; rev ^= 1;
     g1.kspread = 1;
-    if ((rc = launch_gemm<EPI_STORE, 1>(g1, batch, stream, "ns K1 (T^T T)"))) return rc;
+    if ((rc = launch_gemm<EPI_STORE, 1>(g1, tl[0], d.mp, d.mp, batch, stream, "ns K1 (T^T T)")))
+      return rc;
     // K2: B = b A + c A A
     GemmArgs g2 = g1;
     g2.P = Am; g2.p_bs = (long long)d.mp * d.mp; g2.p_rows = d.mp;
@@ -944,12 +1016,14 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     g2.out = Bm; g2.outT = Bm;
     g2.rev = rev; rev ^= 1;
     g2.kspread = 0;
-    if ((rc = launch_gemm<EPI_POLY, 0>(g2, batch, stream, "ns K2 (bA + cA^2 + aI)"))) return rc;
+    if ((rc = launch_gemm<EPI_POLY, 0>(g2, tl[1], d.mp, d.mp, batch, stream,
+                                      "ns K2 (bA + cA^2 + aI)")))
+      return rc;
     // K3: T' = T B' (the final iterate in the caller's orientation)
     GemmArgs g3{};
     g3.P = Tc; g3.p_bs = (long long)d.np * d.mp; g3.p_rows = d.np;
     g3.Q = Bm; g3.q_bs = (long long)d.mp * d.mp; g3.q_rows = d.mp;
-    g3.K = d.mp; g3.tiles_m = tn; g3.tiles_n = tm; g3.sym = 0;
+    g3.K = d.mp; g3.sym = 0;
     if (!last) {
       g3.out = Tn; g3.out_bs = g3.p_bs; g3.out_rows = d.np;
       g3.valid_i = d.np; g3.valid_j = d.mp;
@@ -962,7 +1036,8 @@ int chain_run_packed(hipStream_t stream, const ChainWs& w, int batch, const Chai
     }
     g3.rev = rev; rev ^= 1;
     g3.kspread = 2;
-    if ((rc = launch_gemm<EPI_STORE, 0>(g3, batch, stream, "ns K3 (T B')"))) return rc;
+    if ((rc = launch_gemm<EPI_STORE, 0>(g3, tl[2], d.np, d.mp, batch, stream, "ns K3 (T B')")))
+      return rc;
     bf16* t = Tc; Tc = Tn; Tn = t;
   }
   return DMH_OK;

@@ -202,7 +202,7 @@ class _DeflatedPolarBase:
         return _native.deflated_polar(A, Omega, kw, GATE_RATIO, DEFLATE_THRESH, self.PAD, hs,
                                       RSVD_NITER, CHOLQR_PASSES, chain_event)
 
-    def polar_groups(self, As, generators, steps=5, chain_events=None):
+    def polar_groups(self, As, generators, steps=5, chain_events=None, chain_window=None):
         """polar_group over the tall shape groups of one optimizer step, with one
         generator per group; returns [(polar factors, k, d)] in group order.
 
@@ -213,8 +213,13 @@ class _DeflatedPolarBase:
         With chain_events (a list of (start, end) torch.cuda.Event pairs, one per group)
         the chains instead run one after the other on the current stream once every
         front-end has finished, with pair g recorded around group g's chain, so that
-        the chains' time can be measured alone.  Every group's sketch comes from its
-        own generator and every result equals that of a polar_group call."""
+        the chains' time can be measured alone.  With chain_window (one (start, end)
+        pair) every front-end finishes first, then the chains run together, each on
+        its group's stream, with start recorded on the current stream before them and
+        end after all of them: the time of the chain phase of the step with the
+        groups' chains overlapping each other but no front-end.  Every group's sketch
+        comes from its own generator and every result equals that of a polar_group
+        call."""
         hs = self._fused(steps)
         if hs is None or len(As) < 2 or not As[0].is_cuda:
             # one group after the other (an arm with its own clip or iteration: the
@@ -232,7 +237,7 @@ class _DeflatedPolarBase:
         dev = As[0].device
         main = torch.cuda.current_stream(dev)
         side = _side_streams(dev, len(As))
-        concurrent_chains = not chain_events
+        concurrent_chains = not chain_events and chain_window is None
         # the largest group (the critical path) is enqueued first
         order = sorted(range(len(As)), key=lambda gi: -As[gi].numel())
         fronts = [None] * len(As)
@@ -257,6 +262,18 @@ class _DeflatedPolarBase:
         for s in side:
             main.wait_stream(s)
         if concurrent_chains:
+            return outs
+        if chain_window is not None:
+            chain_window[0].record(main)
+            for s, gi in zip(side, order):
+                s.wait_stream(main)
+                with torch.cuda.stream(s):
+                    U = _native.deflated_polar_chain(fronts[gi], hs)
+                U.record_stream(main)
+                outs[gi] = (U, fronts[gi].k, fronts[gi].d)
+            for s in side:
+                main.wait_stream(s)
+            chain_window[1].record(main)
             return outs
         for gi, fr in enumerate(fronts):
             ev = chain_events[gi]

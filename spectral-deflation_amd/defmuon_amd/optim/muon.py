@@ -37,6 +37,32 @@ def zeropower_via_newtonschulz5(G, steps):
     return out.reshape(G.shape)
 
 
+def plain_group_chains(stacks, talls, entry_mode, sched):
+    """The plain arm's chain (ns_chain with entry normalisation) over each stacked
+    group, [polar factors] in group order.  With several groups on a GPU every group
+    runs on a side stream of its own, the largest first: a small group's launches
+    leave most compute units idle, which the other groups' launches fill.  Each result
+    equals that of ns_chain on its group alone."""
+    if len(stacks) < 2 or not stacks[0].is_cuda:
+        return [_native.ns_chain(X, t, entry_mode, sched) for X, t in zip(stacks, talls)]
+    from defmuon_amd.optim.deflation_batched import _side_streams
+    dev = stacks[0].device
+    main = torch.cuda.current_stream(dev)
+    order = sorted(range(len(stacks)), key=lambda i: -stacks[i].numel())
+    outs = [None] * len(stacks)
+    side = _side_streams(dev, len(stacks))
+    for s in side:
+        s.wait_stream(main)
+    for s, i in zip(side, order):
+        with torch.cuda.stream(s):
+            outs[i] = _native.ns_chain(stacks[i], talls[i], entry_mode, sched)
+        stacks[i].record_stream(s)
+        outs[i].record_stream(main)
+    for s in side:
+        main.wait_stream(s)
+    return outs
+
+
 _EXCLUDED = ("embeddings", "embed_tokens", "wte", "lm_head", "wpe")
 
 
@@ -324,9 +350,12 @@ class Muon(torch.optim.Optimizer):
             tall = gq.size(0) > gq.size(1) if mode == 1 else gq.size(-2) > gq.size(-1)
             X = as_batch(gq)
             groups.setdefault((tuple(X.shape[1:]), X.dtype, tall), []).append((p, g, X))
-        for (_, _, tall), es in groups.items():
-            stack = es[0][2] if len(es) == 1 else torch.cat([X for _, _, X in es])
-            out = _native.ns_chain(stack, tall, mode, sched)
+        keys = list(groups)
+        stacks = [groups[k][0][2] if len(groups[k]) == 1 else torch.cat([X for _, _, X in groups[k]])
+                  for k in keys]
+        outs = plain_group_chains(stacks, [k[2] for k in keys], mode, sched)
+        for key, out in zip(keys, outs):
+            es = groups[key]
             off = 0
             for p, g, X in es:
                 u = out[off:off + X.shape[0]].reshape(g.shape)

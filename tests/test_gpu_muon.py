@@ -182,8 +182,9 @@ def test_cutoff_switches_to_plain_arm(muon_mod, monkeypatch):
 @pytest.mark.parametrize("arm", ["deflated_ns_cut", "deflated_pe_cut"])
 def test_polar_groups_equal_per_group_calls(arm):
     """polar_groups (one stream per shape group; the chains either on the groups'
-    streams or, with chain events, in turn on the current stream) gives bit for bit
-    the per-group polar_group results: polar factors, gate widths k and divisors d."""
+    streams, or with chain events in turn on the current stream, or with a chain
+    window together after every front-end) gives bit for bit the per-group
+    polar_group results: polar factors, gate widths k and divisors d."""
     from defmuon_amd import synthetic as S
     from defmuon_amd.optim import deflation_cutoff as C
     fac = C.ARMS[arm]()
@@ -202,9 +203,12 @@ def test_polar_groups_equal_per_group_calls(arm):
     evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in As]
     got_seq = fac.polar_groups(As, gens(), steps=5, chain_events=evs)   # chains in turn
     got = fac.polar_groups(As, gens(), steps=5)                          # chains per stream
+    win = tuple(torch.cuda.Event(enable_timing=True) for _ in range(2))
+    got_win = fac.polar_groups(As, gens(), steps=5, chain_window=win)    # chains together
     want = [fac.polar_group(A, generator=g, steps=5) for A, g in zip(As, gens())]
     torch.cuda.synchronize()
-    for res in (got_seq, got):
+    assert win[0].elapsed_time(win[1]) > 0.0
+    for res in (got_seq, got, got_win):
         for gi, ((u1, k1, d1), (u2, k2, d2)) in enumerate(zip(res, want)):
             assert torch.equal(k1, k2), (gi, k1, k2)
             assert torch.equal(d1, d2), (gi, d1, d2)

@@ -43,6 +43,40 @@ def test_single_products_match_fp64(N, shape):
     assert rel(out, A @ Xd) < 2e-2
 
 
+TILE_CHOICES = ["256,256,256", "128,128,128", "128,128,256"]
+
+
+@pytest.mark.parametrize("tiles", TILE_CHOICES[1:])
+@pytest.mark.parametrize("shape", [(1, 256, 512), (2, 320, 96), (1, 512, 256), (2, 768, 384)])
+def test_single_products_match_fp64_small_tiles(N, shape, tiles, monkeypatch):
+    """The 128 x 128-tile GEMMs (the m x m products of small matrices) read and write
+    the same layouts as the 256 x 256 ones: the single products of each phase against
+    fp64."""
+    monkeypatch.setenv("DMH_CHAIN_TILES", tiles)
+    test_single_products_match_fp64(N, shape)
+
+
+@pytest.mark.parametrize("shape", [(4, 1024, 512), (6, 768, 768), (3, 520, 264)])
+def test_tile_sizes_agree(N, shape, monkeypatch):
+    """The chain on 256 x 256 and on 128 x 128 output tiles (which only changes each
+    output's K-walk order) gives the same polar factor to the oracle's parity bounds,
+    and the two agree with each other within bf16 rounding of the chain."""
+    from defmuon_amd import synthetic as S
+    B, n, m = shape
+    A = torch.stack([S.spiked_matrix(n, m, seed=31 * b + n, n_spikes=3, hi=50.0, lo=20.0)
+                     for b in range(B)])
+    X0 = (A / (A.norm(dim=(-2, -1), keepdim=True) + 1e-7)).bfloat16()
+    want = O.horner_iterate(X0, O.ns_schedule(5))
+    outs = {}
+    for tiles in TILE_CHOICES:
+        monkeypatch.setenv("DMH_CHAIN_TILES", tiles)
+        outs[tiles] = N.ns_chain(X0.to(DEV), True, 0, O.ns_schedule(5)).cpu()
+        for b in range(B):
+            assert_polar_parity(outs[tiles][b], want[b], A[b], tag=f"tiles {tiles} {shape} {b}")
+    for tiles in TILE_CHOICES[1:]:
+        assert rel(outs[tiles], outs[TILE_CHOICES[0]]) < 6e-2, tiles
+
+
 def test_zero_steps_and_entry(N):
     G = torch.randn(2, 96, 160, generator=torch.Generator().manual_seed(3))
     for mode, scale in ((1, 1.0), (2, 1.01)):
