@@ -434,11 +434,13 @@ def summarize_trace(path, workload, rounds):
               f"{gbs:.0f} | {gbs / PEAK_HBM_GBS:.2f} |")
 
 
-GEMM_LABELS = {
-    "dmh::gemm_nt_bf16<0, 0>": "K3 T' = T B'",
-    "dmh::gemm_nt_bf16<0, 1>": "K1 A = T^T T, K-major",
-    "dmh::gemm_nt_bf16<1, 0>": "K2 B' = bA + cA^2 + aI",
-}
+GEMM_LABELS = {}
+for _tl in (256, 128):
+    GEMM_LABELS.update({
+        f"dmh::gemm_nt_bf16<0, 0, {_tl}>": f"K3 T' = T B', {_tl}x{_tl} tiles",
+        f"dmh::gemm_nt_bf16<0, 1, {_tl}>": f"K1 A = T^T T, K-major, {_tl}x{_tl} tiles",
+        f"dmh::gemm_nt_bf16<1, 0, {_tl}>": f"K2 B' = bA + cA^2 + aI, {_tl}x{_tl} tiles",
+    })
 
 
 def _dmh_kernel(name):
@@ -459,14 +461,15 @@ def summarize_step_trace(path, steps, warmup):
     """Per-polar-step table of the library's kernels from a rocprofv3 --kernel-trace
     kernel_trace.csv (plain or .gz) of `bench.py --steps S --warmup W`: the chain's
     GEMMs over the S steps of the sequential pass (launch stream, Stream_Id 0), every
-    other kernel over all W + 2S steps."""
+    other kernel over all W + 3S steps (warm-up, timed steps, the two NS-chain
+    passes)."""
     import collections
     import csv
     import gzip
     opener = gzip.open if path.endswith(".gz") else open
     with opener(path, "rt") as f:
         rows = list(csv.DictReader(f))
-    all_steps = warmup + 2 * steps
+    all_steps = warmup + 3 * steps
     agg = collections.OrderedDict()
     for r in rows:
         k = _dmh_kernel(r["Kernel_Name"])
@@ -496,8 +499,8 @@ def summarize_step_trace(path, steps, warmup):
 
 def summarize_pmc(paths, steps_in_trace, copy_mib=0, traffic_json=None):
     """Per-kernel sums of rocprofv3 --pmc counter_collection.csv files taken over
-    `bench.py --steps S --warmup W` (steps_in_trace = W + S + the S steps of the
-    NS-chain pass), per polar step.  FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are
+    `bench.py --steps S --warmup W` (steps_in_trace = W + S + the 2 S steps of the two
+    NS-chain passes), per polar step.  FETCH_SIZE / WRITE_SIZE (KiB per dispatch) are
     scaled by what they read for torch's copy kernel over --copy-calibration MiB
     (3 copies: FETCH should see the bytes read, WRITE the bytes written); with
     traffic_json the NS chain's traffic per step is written there, stamped with
@@ -511,7 +514,7 @@ def summarize_pmc(paths, steps_in_trace, copy_mib=0, traffic_json=None):
         for r in csv.DictReader(open(path)):
             name = r["Kernel_Name"]
             short = ("copy (calibration)" if "copy" in name.lower() and "dmh" not in name else
-                     name.split("(")[0].replace("void ", "").strip())
+                     _dmh_kernel(name) or name.split("(")[0].replace("void ", "").strip())
             key = short
             sums.setdefault(key, collections.defaultdict(float))
             sums[key][r["Counter_Name"]] += float(r["Counter_Value"])
@@ -548,7 +551,8 @@ def summarize_pmc(paths, steps_in_trace, copy_mib=0, traffic_json=None):
             busy = v.get("SQ_BUSY_CU_CYCLES", 0.0)
             util = f" {v.get('SQ_VALU_MFMA_BUSY_CYCLES', 0.0) / (4 * busy):.3f} |" if busy else " - |"
         per_file = max(sum(1 for p, _ in disp[key] if p == path) for path in paths)
-        print(f"| `{key}` | {per_file / steps_in_trace:.1f} | " + " | ".join(cells) + " |" + util)
+        label = f"`{key}`" + (f" ({GEMM_LABELS[key]})" if key in GEMM_LABELS else "")
+        print(f"| {label} | {per_file / steps_in_trace:.1f} | " + " | ".join(cells) + " |" + util)
     if scale:
         print()
         print("scale factors from the copy calibration: " +
@@ -633,7 +637,7 @@ def main():
                          "counters (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.summarize_pmc:
-        summarize_pmc(args.summarize_pmc, args.warmup + 2 * args.steps, args.copy_calibration,
+        summarize_pmc(args.summarize_pmc, args.warmup + 3 * args.steps, args.copy_calibration,
                       args.traffic_json)
         return
     if args.summarize_trace:
