@@ -8,7 +8,8 @@ Polar factors: per group of checks (the tag without its matrix index), the worst
 |relerr(gpu) - relerr(oracle)|, relative orthogonality-residual difference and
 direct difference ||gpu - oracle||_F / ||oracle||_F against their tolerances.
 Front-end: the worst relative singular-value, head-subspace, divisor and entry
-differences."""
+differences.  Convergence study: per iteration dtype and method, the largest difference
+of a relative-error curve point from the oracle's."""
 
 import json
 import re
@@ -21,10 +22,16 @@ from parity import DIRECT_TOL, ORTH_TOL, POLAR_TOL  # noqa: E402
 
 
 def main(path):
-    polar, front = OrderedDict(), OrderedDict()
+    polar, front, conv = OrderedDict(), OrderedDict(), OrderedDict()
     for line in open(path):
         r = json.loads(line)
-        if r["kind"] == "polar":
+        if r["kind"] == "convergence":
+            words = r["tag"].split(" ")   # "<dtype> <step> <matrix> <method>"
+            dtype, method = words[0], words[-1]
+            g = conv.setdefault((dtype, method), dict(n=0, diff=0.0))
+            g["n"] += 1
+            g["diff"] = max(g["diff"], r["max_curve_diff"])
+        elif r["kind"] == "polar":
             key = re.sub(r"(\s*#\d+|\[\d+\])$", "", r["tag"])
             g = polar.setdefault(key, dict(n=0, drel=0.0, dorth=0.0, direct=0.0, relerr=0.0))
             g["n"] += 1
@@ -51,6 +58,13 @@ def main(path):
         for key, g in front.items():
             f = lambda k: f"{g[k]:.2e}" if k in g else "-"
             print(f"| {key} | {f('s')} | {f('head')} | {f('d')} | {f('x0')} |")
+    if conv:
+        print()
+        print("| convergence curves (iteration dtype, method) | curves | max point difference "
+              "from the oracle (tol: bf16 2e-2, fp32 1e-5) |")
+        print("|---|---|---|")
+        for (dtype, method), g in conv.items():
+            print(f"| {dtype} {method} | {g['n']} | {g['diff']:.2e} |")
 
 
 if __name__ == "__main__":
