@@ -632,17 +632,21 @@ __device__ __forceinline__ float4 sk_mov(float4 x) {
 }
 __device__ __forceinline__ float2 sk_mov(float2 x) { return make_float2(sk_mov(x.x), sk_mov(x.y)); }
 
-// Thread t stages the units u = t and t + 256 of a chunk: row c = u / 8, contraction
-// indices k0 + 8 (u % 8) .. +7 (zero at and beyond kend; 8-index groups are whole).
-struct SkStage {
-  float4 v[2][2];
+// A chunk is 512 units: unit u is row c = u / 8, contraction indices k0 + 8 (u % 8) ..
+// +7 (zero at and beyond kend; 8-index groups are whole).  With Q units per thread
+// (2 for a 256-thread workgroup, 1 for 512), thread t stages the units t + (512 / Q) q.
+template <int Q = 2>
+struct SkStageQ {
+  float4 v[Q][2];
 };
+typedef SkStageQ<2> SkStage;
 
-__device__ __forceinline__ void sk_stage_load(SkStage& st, __amdgpu_buffer_rsrc_t sr, int lds,
+template <int Q = 2>
+__device__ __forceinline__ void sk_stage_load(SkStageQ<Q>& st, __amdgpu_buffer_rsrc_t sr, int lds,
                                               int k0, int kend, int tid) {
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int u = tid + 256 * q;
+  for (int q = 0; q < Q; ++q) {
+    const int u = tid + (512 / Q) * q;
     const int c = u >> 3, k = k0 + 8 * (u & 7);
     const unsigned off = k < kend ? (unsigned)(c * lds + k) * 4u : SK_OOB;
     st.v[q][0] = sk_ld4(sr, off);
@@ -653,9 +657,10 @@ __device__ __forceinline__ void sk_stage_load(SkStage& st, __amdgpu_buffer_rsrc_
 // Keeps the split of a staged chunk at the point of this call: without it the compiler
 // hoists the split to the top of the loop, where it waits for the staging loads just
 // issued and with them for every prefetched load of A.
-__device__ __forceinline__ void sk_pin(SkStage& st) {
+template <int Q = 2>
+__device__ __forceinline__ void sk_pin(SkStageQ<Q>& st) {
 #pragma unroll
-  for (int q = 0; q < 2; ++q)
+  for (int q = 0; q < Q; ++q)
 #pragma unroll
     for (int h = 0; h < 2; ++h)
       asm volatile("" : "+v"(st.v[q][h].x), "+v"(st.v[q][h].y), "+v"(st.v[q][h].z),
@@ -666,11 +671,11 @@ __device__ __forceinline__ void sk_pin(SkStage& st) {
 // order of sk_rows' 16x16 fragments -- within each 32-index step, the 4-index group
 // a = 0..7 at position 8a (a < 4) or 8(a - 4) + 4 (a >= 4), so positions 8g .. 8g + 7
 // hold the indices 4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3.
-template <int SPLITS, bool PERM = false>
-__device__ __forceinline__ void sk_stage_store(const SkStage& st, bf16* buf, int tid) {
+template <int SPLITS, bool PERM = false, int Q = 2>
+__device__ __forceinline__ void sk_stage_store(const SkStageQ<Q>& st, bf16* buf, int tid) {
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int u = tid + 256 * q;
+  for (int q = 0; q < Q; ++q) {
+    const int u = tid + (512 / Q) * q;
     const int c = u >> 3, kk = 8 * (u & 7);
     const float x[8] = {st.v[q][0].x, st.v[q][0].y, st.v[q][0].z, st.v[q][0].w,
                         st.v[q][1].x, st.v[q][1].y, st.v[q][1].z, st.v[q][1].w};
@@ -718,15 +723,20 @@ __device__ __forceinline__ void sk_barrier() {
 // as mfma_split)
 template <int SPLITS>
 __device__ __forceinline__ void mfma_split16(const bf16x8 (&a)[SPLITS], const bf16x8 (&b)[SPLITS],
-                                             f32x4 (&acc)[4], int rb) {
+                                             f32x4& acc) {
   if (SPLITS == 3) {
-    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc[rb], 0, 0, 0);
-    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc[rb], 0, 0, 0);
-    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], acc[rb], 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], acc, 0, 0, 0);
   }
-  acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc[rb], 0, 0, 0);
-  acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc[rb], 0, 0, 0);
-  acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc[rb], 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], acc, 0, 0, 0);
+}
+template <int SPLITS>
+__device__ __forceinline__ void mfma_split16(const bf16x8 (&a)[SPLITS], const bf16x8 (&b)[SPLITS],
+                                             f32x4 (&acc)[4], int rb) {
+  mfma_split16<SPLITS>(a, b, acc[rb]);
 }
 
 // C (n x RP, per matrix) = A (n x m) X, with X given transposed: XT (RP x ldxt),
@@ -854,6 +864,188 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     red[tid] = sq;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
+      if (tid < w) red[tid] += red[tid + w];
+      __syncthreads();
+    }
+    if (tid == 0) asq[(long long)b * gridDim.x + blockIdx.x] = red[0];
+  }
+}
+
+// sk_rows with A streamed global -> LDS by the gfx950 direct-to-LDS load
+// (buffer_load_dwordx4 ... lds) instead of into registers.  Same products, same
+// operands, same order per accumulator, so C is bit-identical to sk_rows'.  Loads that
+// land in registers compete with the MFMAs that read registers: a read-only stream over
+// GPT-2-large's 72 x (5120 x 1280) fp32 that also issues 96 16x16x32 MFMAs per 8 KB per
+// wave ran at 4.1 TB/s with register loads, 5.7 TB/s with the same bytes landing in LDS.
+// WV waves of 256 / WV rows each (8 waves of 32 rows, two per SIMD, one workgroup
+// per compute unit: 457 vs 542 us for 4 waves of 64 rows, one per SIMD, on the tall
+// group; sk_rows 508 us); each wave streams its own rows in stages
+// of 32 contraction indices (128 bytes of each row) through a ring of SKD_NST stages
+// of its own, so the ring needs no workgroup barrier; the small operand is staged and
+// split per 64-index chunk as in sk_rows (one barrier per chunk).  Stage row r holds
+// the row's 16-byte chunk c in slot c ^ ((r >> 1) & 7): the fragment reads (16
+// consecutive rows, one chunk) then cover the 64 banks once.  The per-workgroup sums
+// of squares add the same values in another order (8 waves) than sk_rows.  Needs
+// m % 64 == 0.
+constexpr int SKD_NST = 3;   // A stages in flight per wave
+
+typedef __attribute__((address_space(3))) void* sk_lds_ptr;
+
+__device__ __forceinline__ void sk_load_lds16(__amdgpu_buffer_rsrc_t r, char* lds, int voff,
+                                              int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (sk_lds_ptr)lds, 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ int skd_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+// vmcnt(n) with expcnt and lgkmcnt left at their maxima
+__device__ __forceinline__ void skd_wait_vm(int n) {
+  switch (n) {
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 20: __builtin_amdgcn_s_waitcnt(0x4F74); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+}
+
+template <int SPLITS, int WV>
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(1, 1))) void sk_rows_dtl(
+    const float* __restrict__ A, int n, int m, const float* __restrict__ XT, int ldxt,
+    float* __restrict__ C, double* __restrict__ asq) {
+  constexpr int NT = 64 * WV, RPW = SKR_ROWS / WV, NRB = RPW / 16;
+  constexpr int WSTAGE = RPW * 128;       // bytes of one wave's stage
+  constexpr int LPS = WSTAGE / 1024;      // direct-to-LDS loads per wave and stage
+  constexpr int Q = 512 / NT;             // staging units per thread
+  // Vector memory instructions in issue order: stage s's LPS loads, then s+1's, the
+  // next chunk's 2 Q staging loads, s+2's; so when stage s is read, VM_AFTER issued
+  // after it may still be in flight (the same count at both steps of a chunk).  Stages
+  // past the end are loaded too (into slots nobody reads; rows past the matrix load
+  // zeros), so that count holds to the last step.
+  constexpr int VM_AFTER = 2 * LPS + 2 * Q;
+  static_assert(VM_AFTER == 10 || VM_AFTER == 20, "skd_wait_vm");
+  static_assert(NRB % 2 == 0, "row blocks go in pairs");
+  // One LDS array for the A ring, the staged small operand and the final reduction:
+  // with separate arrays the compiler tags their accesses with alias scopes and then
+  // makes every read of the ring wait for all direct-to-LDS loads in flight
+  // (vmcnt(0)), which would leave no stage in flight; the waits here are explicit.
+  __shared__ __attribute__((aligned(1024))) char smem[SKD_NST * WV * WSTAGE + 2 * SK_BUF * 2];
+  char* const aring = smem;
+  bf16* const xl = (bf16*)(smem + SKD_NST * WV * WSTAGE);
+  const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int r0 = blockIdx.x * SKR_ROWS + wave * RPW;
+  A += (long long)b * n * m;
+  XT += (long long)b * RP * ldxt;
+  C += (long long)b * n * RP;
+  // the wave's rows only: rows at or past n load zeros
+  const int rh = n - r0;
+  const int rows_here = __builtin_amdgcn_readfirstlane(rh < 0 ? 0 : (rh > RPW ? RPW : rh));
+  const __amdgpu_buffer_rsrc_t ar =
+      sk_rsrc(A + (long long)(rh > 0 ? r0 : 0) * m, (long long)rows_here * m);
+  const __amdgpu_buffer_rsrc_t xr = sk_rsrc(XT, (long long)RP * ldxt);
+  // load q of a stage: rows 8 q + lane / 8, the row's chunk (lane % 8) ^ swizzle into
+  // LDS slot lane % 8 (the stage's k offset goes in the scalar offset)
+  int voff[LPS];
+#pragma unroll
+  for (int q = 0; q < LPS; ++q) {
+    const int r = 8 * q + lane / 8;
+    voff[q] = r * m * 4 + skd_slot(r, lane % 8) * 16;
+  }
+  char* const wring = aring + wave * WSTAGE;   // slot j at wring + j * WV * WSTAGE
+#define SKD_ISSUE(s_)                                                                  \
+  do {                                                                                 \
+    char* dst_ = wring + ((s_) % SKD_NST) * WV * WSTAGE;                               \
+    _Pragma("unroll") for (int q = 0; q < LPS; ++q)                                    \
+      sk_load_lds16(ar, dst_ + q * 1024, voff[q], (s_) * 128);                         \
+  } while (0)
+  // the lane's fragment offsets within a stage: row 16 rb + l16, chunks g and 4 + g
+  int foff[NRB][2];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = 16 * rb + l16;
+      foff[rb][h] = r * 128 + skd_slot(r, 4 * h + g) * 16;
+    }
+  f32x4 acc[4][NRB];   // [cb][rb]
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[cb][rb][e] = 0.f;
+  double sq = 0.0;
+  const int nch = m / SK_KC;
+  // (the next chunk's staging loads are issued and consumed within one iteration:
+  // carried across the loop's back edge, their registers were copied at the loop head,
+  // which waited for them)
+  {
+    SkStageQ<Q> stg;
+    sk_stage_load<Q>(stg, xr, ldxt, 0, m, tid);
+    sk_stage_store<SPLITS, true, Q>(stg, xl, tid);
+  }
+  SKD_ISSUE(0);
+  SKD_ISSUE(1);
+  sk_barrier();
+  for (int ch = 0; ch < nch; ++ch) {
+    const bf16* buf = xl + (ch & 1) * SK_BUF;
+    SkStageQ<Q> stg;
+    sk_stage_load<Q>(stg, xr, ldxt, (ch + 1) * SK_KC, m, tid);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int ks = 2 * ch + p;
+      SKD_ISSUE(ks + 2);
+      skd_wait_vm(VM_AFTER);   // stage ks has landed
+      const char* st = wring + (ks % SKD_NST) * WV * WSTAGE;
+#pragma unroll
+      for (int rp = 0; rp < NRB; rp += 2) {
+        bf16x8 as[2][SPLITS];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const f32x4 lo = *(const f32x4*)(st + foff[rp + u][0]);
+          const f32x4 hi = *(const f32x4*)(st + foff[rp + u][1]);
+          const float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          if (asq) {
+            float f = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f = fmaf(v[e], v[e], f);
+            sq += (double)f;
+          }
+          split_bf16<SPLITS>(v, as[u]);
+        }
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          bf16x8 xs[SPLITS];
+#pragma unroll
+          for (int s = 0; s < SPLITS; ++s)
+            xs[s] = *(const bf16x8*)(buf + s * SK_TERM + (16 * cb + l16) * SK_PITCH + 32 * p + 8 * g);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) mfma_split16<SPLITS>(xs, as[u], acc[cb][rp + u]);
+        }
+      }
+    }
+    sk_pin<Q>(stg);
+    sk_stage_store<SPLITS, true, Q>(stg, xl + ((ch + 1) & 1) * SK_BUF, tid);
+    sk_barrier();
+  }
+#undef SKD_ISSUE
+  // every load issued has landed before the wave ends (the last ones fill unread slots)
+  skd_wait_vm(0);
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb) {
+    const int i = r0 + 16 * rb + l16;
+    if (i >= n) continue;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+      *(float4*)&C[(long long)i * RP + 16 * cb + 4 * g] =
+          make_float4(acc[cb][rb][0], acc[cb][rb][1], acc[cb][rb][2], acc[cb][rb][3]);
+  }
+  if (asq) {
+    double* red = (double*)smem;   // the ring is no longer read
+    __syncthreads();
+    red[tid] = sq;
+    __syncthreads();
+    for (int w = NT / 2; w > 0; w >>= 1) {
       if (tid < w) red[tid] += red[tid + w];
       __syncthreads();
     }
@@ -2284,7 +2476,13 @@ static int orth(hipStream_t st, const float* Y, float* Q, float* tmp, int B, int
 static int skr(hipStream_t st, const float* A, int B, int n, int m, const float* XT, float* Y,
                double* asq) {
   dim3 grid(ceil_div(n, SKR_ROWS), B);
-  hipLaunchKernelGGL(sk_rows<3>, grid, dim3(256), 0, st, A, n, m, XT, m, Y, asq);
+  // the direct-to-LDS variant needs whole 64-index chunks; DMH_SKR_DTL=0 selects the
+  // register-load kernel (same results) for comparisons
+  const char* e = getenv("DMH_SKR_DTL");
+  if (m % SK_KC == 0 && !(e && e[0] == '0'))
+    hipLaunchKernelGGL((sk_rows_dtl<3, 8>), grid, dim3(512), 0, st, A, n, m, XT, m, Y, asq);
+  else
+    hipLaunchKernelGGL(sk_rows<3>, grid, dim3(256), 0, st, A, n, m, XT, m, Y, asq);
   DMH_CHECK_LAUNCH("sk_rows");
   return DMH_OK;
 }

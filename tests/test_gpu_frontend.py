@@ -352,3 +352,29 @@ def test_clip_threshold_below_ratio(N):
     assert kw == 13
     k, ko, k8 = _clip_vs_fp64(N, A, kw, 0.10, 0.04, "clip thresh 0.04 < ratio 0.10")
     assert k == ko == k8 == [16, 16, 16]
+
+
+@pytest.mark.parametrize("B,n,m", [(3, 1000, 768), (2, 3072, 768), (2, 1280, 1280), (1, 264, 128)])
+def test_skinny_rows_direct_to_lds_matches_register_kernel(N, B, n, m, monkeypatch):
+    """The direct-to-LDS A x X kernel (rows of A streamed through an LDS ring, the
+    default where m % 64 == 0) and the register-load kernel (DMH_SKR_DTL=0) make the
+    same products in the same order: the rSVD outputs are bit-identical (partial last
+    row blocks included).  Their per-workgroup sums of squares of A, behind the
+    divisor, add the same values in another order, so k is equal and d and X0 agree
+    to fp32 rounding."""
+    from defmuon_amd import synthetic as S
+    A = torch.stack([S.spiked_matrix(n, m, seed=7 * b + n, n_spikes=4, hi=40.0, lo=12.0)
+                     for b in range(B)]).to(DEV)
+    r, kw = O.sketch_dims(m)
+    Om = O.draw_omega(B, m, r, 99).to(DEV)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("DMH_SKR_DTL", mode)
+        X0, k, d = N.rmfro_clip(A, Om, kw, O.GATE_RATIO, O.DEFLATE_THRESH, O.DIVISOR_PAD, 1, 1)
+        U, s, V = N.rsvd(A, Om, 1, 1)
+        outs[mode] = [t.cpu() for t in (X0, k, d, U, s, V)]
+    (X0r, kr, dr, Ur, sr, Vr), (X0, k, d, U, s, V) = outs["0"], outs["1"]
+    for a, b in ((U, Ur), (s, sr), (V, Vr), (k, kr)):
+        assert torch.equal(a, b)
+    assert float(((d - dr).abs() / dr).max()) < 1e-6
+    assert rel(X0, X0r) < 1e-6
