@@ -361,6 +361,10 @@ KERNEL_BYTES = {
     "momentum_stack": 16,    # grad and buffer read, buffer and fp32 stack written
     "apply_update": 10,      # parameter read and written fp32, bf16 update read
 }
+# (read, written) bytes per element of the same kernels
+KERNEL_RW = {"sk_rows": (4, 0), "sk_cols": (4, 0), "deflate_restore": (4, 2),
+             "entry_norm_partials": (4, 0), "entry_pack": (4, 2), "momentum_stack": (8, 8),
+             "apply_update": (6, 4)}
 
 
 def kernels_report(args, dev):
@@ -432,6 +436,50 @@ def summarize_trace(path, workload, rounds):
         gbs = nbytes / tot_ns
         print(f"| `{name}` | {calls} | {tot_ns / calls / 1e3:.1f} | {nbytes / calls / 1e9:.3f} | "
               f"{gbs:.0f} | {gbs / PEAK_HBM_GBS:.2f} |")
+
+
+def summarize_kernel_traffic(paths, workload, rounds, copy_mib):
+    """HBM bytes the memory-bound kernels moved, from two rocprofv3 --pmc runs of
+    `bench.py --mode kernels --copy-calibration MIB` (FETCH_SIZE, then WRITE_SIZE, KiB per
+    dispatch, each scaled by what it reads for torch's copy kernel of known size),
+    against the algorithmic bytes (KERNEL_RW per element) of the same launches."""
+    import collections
+    import csv
+    groups = WORKLOADS[workload]
+    elems = sum(B * n * m for B, n, m in groups)
+    per_round_launches = {"sk_rows": 2, "sk_cols": 2}
+    sums = collections.defaultdict(lambda: collections.defaultdict(float))
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"]
+            if "copy" in name.lower() and "dmh" not in name:
+                key = "copy"
+            else:
+                key = next((k for k in KERNEL_RW if k in name), None)
+            if key:
+                sums[key][r["Counter_Name"]] += float(r["Counter_Value"]) * 1024
+    scale = {}
+    cal = sums.get("copy", {})
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        if copy_mib and cal.get(c):
+            scale[c] = 3 * copy_mib * 2 ** 20 / cal[c]
+    print("| kernel | algorithmic GB read / written per round | measured GB fetched / written "
+          "per round | fetched / algorithmic read | written / algorithmic write |")
+    print("|---|---|---|---|---|")
+    for name, (rd, wr) in KERNEL_RW.items():
+        if name not in sums:
+            continue
+        n = rounds * per_round_launches.get(name, 1)
+        a_rd, a_wr = rd * elems * n / rounds / 1e9, wr * elems * n / rounds / 1e9
+        f = sums[name].get("FETCH_SIZE", 0.0) * scale.get("FETCH_SIZE", 1.0) / rounds / 1e9
+        w = sums[name].get("WRITE_SIZE", 0.0) * scale.get("WRITE_SIZE", 1.0) / rounds / 1e9
+        fr = f"{f / a_rd:.2f}" if a_rd else "-"
+        wrr = f"{w / a_wr:.2f}" if a_wr else "-"
+        print(f"| `{name}` | {a_rd:.3f} / {a_wr:.3f} | {f:.3f} / {w:.3f} | {fr} | {wrr} |")
+    if scale:
+        print()
+        print("scale factors from the copy calibration: " +
+              ", ".join(f"{c} x{v:.3f}" for c, v in scale.items()))
 
 
 GEMM_LABELS = {}
@@ -631,6 +679,10 @@ def main():
                     help="print the per-polar-step table of the library's kernels from a "
                          "rocprofv3 --kernel-trace kernel_trace.csv (or .csv.gz) taken over "
                          "this bench with the same --steps/--warmup")
+    ap.add_argument("--summarize-kernel-traffic", nargs="+", metavar="COUNTER_CSV",
+                    help="tabulate rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of --mode kernels "
+                         "against the memory-bound kernels' algorithmic bytes (with the same "
+                         "--workload/--steps/--warmup/--copy-calibration)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="before the steps, copy a MIB-MiB fp32 buffer three times with "
                          "torch's copy kernel: a known-size reference for HBM byte "
@@ -642,6 +694,10 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.workload, args.warmup + args.steps)
+        return
+    if args.summarize_kernel_traffic:
+        summarize_kernel_traffic(args.summarize_kernel_traffic, args.workload,
+                                 args.warmup + args.steps, args.copy_calibration)
         return
     if args.summarize_step_trace:
         summarize_step_trace(args.summarize_step_trace, args.steps, args.warmup)
@@ -661,6 +717,14 @@ def main():
         sys.exit(1)
     _native.load()
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration * 2 ** 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: copy calibration: 3 x {args.copy_calibration} MiB read + written")
+        del src, dst
     if args.mode == "train":
         print(json.dumps(train_step_report(args, dev)), flush=True)
         return
@@ -673,14 +737,6 @@ def main():
         sys.exit(2)
     groups = WORKLOADS.get(args.workload)
     fac = None if plain else C.ARMS[args.arm]()
-    if args.copy_calibration:
-        src = torch.ones(args.copy_calibration * 2 ** 18, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"bench: copy calibration: 3 x {args.copy_calibration} MiB read + written")
-        del src, dst
     if plain:
         pgroups = PLAIN_GROUPS[args.workload]
         log(f"bench: generating inputs for {args.workload} ({args.arm}): {pgroups}")
