@@ -414,6 +414,44 @@ def kernels_report(args, dev):
             "rounds": args.warmup + args.steps}
 
 
+def horner_f32_report(args, dev):
+    """--mode horner-f32: the fp32 iteration (`_horner_iterate` on fp32 input, the
+    path the reference's convergence study runs; dmh_horner_f32 on the fp32 matrix
+    cores) over the workload's shape groups, 5 NS steps per matrix, the groups one
+    after the other on the launch stream; `args.steps` timed rounds after
+    `args.warmup`.  FLOP: the canonical 4m^2n + 2m^3 per matrix and step."""
+    import torch
+    from defmuon_amd.optim import deflation_batched as DB
+    groups = WORKLOADS[args.workload]
+    hs = [DB.DeflatedNSPolar.NS_ABC] * 5
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    xs = []
+    for B, n, m in groups:
+        X = torch.randn(B, n, m, device=dev, generator=gen)
+        xs.append(X / X.norm(dim=(-2, -1), keepdim=True))
+    for _ in range(args.warmup):
+        for X in xs:
+            DB._horner_iterate(X, hs)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        for X in xs:
+            DB._horner_iterate(X, hs)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    flop = sum(B * (4 * m * m * n + 2 * m ** 3) * len(hs) for B, n, m in groups)
+    tflops = flop / ms / 1e9
+    log(f"bench horner-f32: {args.warmup} + {args.steps} rounds over {groups}")
+    return {"mode": "horner-f32", "workload": args.workload, "groups": groups,
+            "ms_per_step": round(ms, 3), "flop_per_step": flop, "tflops": round(tflops, 1),
+            "frac_fp32_mfma_peak": round(tflops / 157.3, 3), "steps": args.steps,
+            "warmup": args.warmup}
+
+
 def summarize_trace(path, workload, rounds):
     """GB/s of the memory-bound kernels from a rocprofv3 --stats kernel_stats.csv of
     `bench.py --mode kernels` (algorithmic bytes KERNEL_BYTES per element, summed
@@ -660,11 +698,14 @@ def main():
                     help="synthetic momenta: spiked spectra generated on the GPU (default), "
                          "the same generated on the host (counter runs: no GPU solver "
                          "call), or i.i.d. Gaussian")
-    ap.add_argument("--mode", default="polar", choices=["polar", "train", "kernels"],
+    ap.add_argument("--mode", default="polar",
+                    choices=["polar", "train", "kernels", "horner-f32"],
                     help="polar: the polar-step bench (default); train: the GPT-2-large "
                          "training step of config 5, with the polar-factor share; kernels: "
                          "the memory-bound kernels one after the other, for a rocprofv3 "
-                         "kernel trace (see --summarize-trace)")
+                         "kernel trace (see --summarize-trace); horner-f32: the fp32 "
+                         "iteration (the convergence study's path) over the workload's "
+                         "shape groups")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="COUNTER_CSV",
                     help="print per-kernel counter sums per polar step of rocprofv3 --pmc "
                          "counter_collection.csv files taken over this bench with the same "
@@ -730,6 +771,9 @@ def main():
         return
     if args.mode == "kernels":
         print(json.dumps(kernels_report(args, dev)), flush=True)
+        return
+    if args.mode == "horner-f32":
+        print(json.dumps(horner_f32_report(args, dev)), flush=True)
         return
     plain = args.arm in ("ns5", "polarexpress")
     if (plain and args.workload not in PLAIN_GROUPS) or (not plain and args.workload not in WORKLOADS):
