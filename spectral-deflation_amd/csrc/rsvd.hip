@@ -554,6 +554,8 @@ __device__ __forceinline__ void gram_mfma(const float4 (&v)[GRAM_G], f64x4 (&acc
   }
 }
 
+// STAGE: the partial leaves through LDS (for short chunks: GRAM_STAGE_ROWS rows or less)
+template <bool STAGE>
 __device__ __forceinline__ void gram_chunk(const float* __restrict__ Y, int rows, long long y_bs,
                                            double* __restrict__ part, int b, int chunk, int l) {
   const int per = (rows + GRAM_CHUNKS - 1) / GRAM_CHUNKS;
@@ -586,36 +588,74 @@ __device__ __forceinline__ void gram_chunk(const float* __restrict__ Y, int rows
     asm volatile("" ::: "memory");
   }
   double* out = part + ((long long)b * GRAM_CHUNKS + chunk) * RP * RP;
-  int t = 0;
+  if constexpr (!STAGE) {   // long chunks: the stores are a small part, straight from registers
+    int t = 0;
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int c2 = c; c2 < 4; ++c2, ++t)
+      for (int c2 = c; c2 < 4; ++c2, ++t)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int p = 4 * (kr + 4 * e) + c, q = cq + c2;
-        out[p * RP + q] = acc[t][e];
-        if (c != c2) out[q * RP + p] = acc[t][e];
-      }
+        for (int e = 0; e < 4; ++e) {
+          const int p = 4 * (kr + 4 * e) + c, q = cq + c2;
+          out[p * RP + q] = acc[t][e];
+          if (c != c2) out[q * RP + p] = acc[t][e];
+        }
+  } else {
+  // Short chunks: the partial leaves through LDS, 32 rows at a time, as whole 512-byte
+  // rows (from the accumulators, the mirrored entries are 8-byte stores scattered over
+  // 16 rows per instruction: a fifth of the kernel's time at 160-row chunks; at 640
+  // rows the LDS kernel is 4% slower, so long chunks keep the stores from registers).
+  __shared__ __attribute__((aligned(16))) double S[32][RP + 2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int t = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int c2 = c; c2 < 4; ++c2, ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int p = 4 * (kr + 4 * e) + c, q = cq + c2;
+          if ((p >> 5) == h) S[p & 31][q] = acc[t][e];
+          if (c != c2 && (q >> 5) == h) S[q & 31][p] = acc[t][e];
+        }
+    __syncthreads();
+    // lane l: doubles 2 (l % 32), +1 of rows 2 i + l / 32 of this half
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = 2 * i + (l >> 5), col = 2 * (l & 31);
+      *(double2*)&out[(32 * h + row) * RP + col] = *(const double2*)&S[row][col];
+    }
+    __syncthreads();
+  }
+  }
 }
 
-// grid (GRAM_CHUNKS, batch)
+constexpr int GRAM_STAGE_ROWS = 256;
+__host__ __device__ constexpr bool gram_stage(int rows) {
+  return (rows + GRAM_CHUNKS - 1) / GRAM_CHUNKS <= GRAM_STAGE_ROWS;
+}
+
+// grid (GRAM_CHUNKS, batch); STAGE = gram_stage(rows)
+template <bool STAGE>
 __global__ __launch_bounds__(64) void gram_partials(const float* __restrict__ Y, int rows,
                                                     long long y_bs, double* __restrict__ part) {
-  gram_chunk(Y, rows, y_bs, part, blockIdx.y, blockIdx.x, threadIdx.x);
+  gram_chunk<STAGE>(Y, rows, y_bs, part, blockIdx.y, blockIdx.x, threadIdx.x);
 }
 
 // two independent Gram partials in one launch (Bp Bp^T and Q^T Q before the gate):
 // grid (2 GRAM_CHUNKS, batch)
+// S1, S2 = gram_stage(rows1), gram_stage(rows2)
+template <bool S1, bool S2>
 __global__ __launch_bounds__(64) void gram_partials_pair(const float* __restrict__ Y1, int rows1,
                                                          double* __restrict__ part1,
                                                          const float* __restrict__ Y2, int rows2,
                                                          double* __restrict__ part2) {
   if ((int)blockIdx.x < GRAM_CHUNKS)
-    gram_chunk(Y1, rows1, (long long)rows1 * RP, part1, blockIdx.y, blockIdx.x, threadIdx.x);
+    gram_chunk<S1>(Y1, rows1, (long long)rows1 * RP, part1, blockIdx.y, blockIdx.x, threadIdx.x);
   else
-    gram_chunk(Y2, rows2, (long long)rows2 * RP, part2, blockIdx.y, blockIdx.x - GRAM_CHUNKS,
-               threadIdx.x);
+    gram_chunk<S2>(Y2, rows2, (long long)rows2 * RP, part2, blockIdx.y,
+                   blockIdx.x - GRAM_CHUNKS, threadIdx.x);
 }
 
 // A copy the compiler cannot fold away: a prefetch slot is copied out before its next
@@ -2434,8 +2474,12 @@ static int sg(hipStream_t st, int mode, const float* A, int B, int n, int m, con
 }
 
 static int gram(hipStream_t st, const float* Y, int B, int rows, double* part) {
-  hipLaunchKernelGGL(gram_partials, dim3(GRAM_CHUNKS, B), dim3(64), 0, st, Y, rows,
-                     (long long)rows * RP, part);
+  if (gram_stage(rows))
+    hipLaunchKernelGGL(gram_partials<true>, dim3(GRAM_CHUNKS, B), dim3(64), 0, st, Y, rows,
+                       (long long)rows * RP, part);
+  else
+    hipLaunchKernelGGL(gram_partials<false>, dim3(GRAM_CHUNKS, B), dim3(64), 0, st, Y, rows,
+                       (long long)rows * RP, part);
   DMH_CHECK_LAUNCH("gram_partials");
   return DMH_OK;
 }
@@ -2563,8 +2607,16 @@ static int rsvd_core(hipStream_t st, const float* A, const float* Omega, int B, 
   }
   // H = Bp Bp^T = Gram of Bp^T (and Q^T Q for d, in the same launch)
   if (d) {
-    hipLaunchKernelGGL(gram_partials_pair, dim3(2 * GRAM_CHUNKS, B), dim3(64), 0, st, w.Bt, m,
-                       w.gram, w.Q, n, w.gramq);
+    const dim3 gg(2 * GRAM_CHUNKS, B);
+    if (gram_stage(m) && gram_stage(n))
+      hipLaunchKernelGGL((gram_partials_pair<true, true>), gg, dim3(64), 0, st, w.Bt, m, w.gram,
+                         w.Q, n, w.gramq);
+    else if (gram_stage(m))
+      hipLaunchKernelGGL((gram_partials_pair<true, false>), gg, dim3(64), 0, st, w.Bt, m, w.gram,
+                         w.Q, n, w.gramq);
+    else
+      hipLaunchKernelGGL((gram_partials_pair<false, false>), gg, dim3(64), 0, st, w.Bt, m,
+                         w.gram, w.Q, n, w.gramq);
     DMH_CHECK_LAUNCH("gram_partials (Bp, Q)");
   } else if ((rc = gram(st, w.Bt, B, m, w.gram))) {
     return rc;
