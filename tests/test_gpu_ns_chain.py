@@ -150,13 +150,15 @@ def test_config2_shape_deflated_iteration(N):
 
 
 @pytest.mark.parametrize("shape,sched", [((2, 320, 96), "ns"), ((1, 768, 256), "pe"),
-                                         ((2, 203, 67), "ns"), ((1, 1030, 130), "pe")])
+                                         ((2, 203, 67), "ns"), ((1, 1030, 130), "pe"),
+                                         ((3, 96, 200), "ns")])
 def test_horner_fp32_keeps_dtype(N, shape, sched):
     """_horner_iterate keeps X's dtype (deflation_batched.py:196-204): fp32 input runs
     the fp32 chain and comes back fp32, within 1e-5 of the oracle's fp32 chain (the
     reference's convergence study runs this function in fp32).  The shapes cover
     partial 128 x 128 output tiles, sizes that are not multiples of 4 (element-wise
-    staging loads instead of 16-byte ones) and a partial last 16-deep K slice."""
+    staging loads instead of 16-byte ones), a partial last 16-deep K slice and a wide
+    input (n < m: G = X^T X is m x m of rank n)."""
     from defmuon_amd.optim import deflation_batched as DB
     g = torch.Generator().manual_seed(sum(shape))
     X = torch.randn(*shape, generator=g)
