@@ -601,33 +601,33 @@ __device__ __forceinline__ void gram_chunk(const float* __restrict__ Y, int rows
           if (c != c2) out[q * RP + p] = acc[t][e];
         }
   } else {
-  // Short chunks: the partial leaves through LDS, 32 rows at a time, as whole 512-byte
-  // rows (from the accumulators, the mirrored entries are 8-byte stores scattered over
-  // 16 rows per instruction: a fifth of the kernel's time at 160-row chunks; at 640
-  // rows the LDS kernel is 4% slower, so long chunks keep the stores from registers).
-  __shared__ __attribute__((aligned(16))) double S[32][RP + 2];
+    // Short chunks: the partial leaves through LDS, 32 rows at a time, as whole 512-byte
+    // rows (from the accumulators, the mirrored entries are 8-byte stores scattered over
+    // 16 rows per instruction: a fifth of the kernel's time at 160-row chunks; at 640
+    // rows the LDS kernel is 4% slower, so long chunks keep the stores from registers).
+    __shared__ __attribute__((aligned(16))) double S[32][RP + 2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    int t = 0;
+    for (int h = 0; h < 2; ++h) {
+      int t = 0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int c2 = c; c2 < 4; ++c2, ++t)
+        for (int c2 = c; c2 < 4; ++c2, ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int p = 4 * (kr + 4 * e) + c, q = cq + c2;
-          if ((p >> 5) == h) S[p & 31][q] = acc[t][e];
-          if (c != c2 && (q >> 5) == h) S[q & 31][p] = acc[t][e];
-        }
-    __syncthreads();
-    // lane l: doubles 2 (l % 32), +1 of rows 2 i + l / 32 of this half
+          for (int e = 0; e < 4; ++e) {
+            const int p = 4 * (kr + 4 * e) + c, q = cq + c2;
+            if ((p >> 5) == h) S[p & 31][q] = acc[t][e];
+            if (c != c2 && (q >> 5) == h) S[q & 31][p] = acc[t][e];
+          }
+      __syncthreads();
+      // lane l: doubles 2 (l % 32), +1 of rows 2 i + l / 32 of this half
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int row = 2 * i + (l >> 5), col = 2 * (l & 31);
-      *(double2*)&out[(32 * h + row) * RP + col] = *(const double2*)&S[row][col];
+      for (int i = 0; i < 16; ++i) {
+        const int row = 2 * i + (l >> 5), col = 2 * (l & 31);
+        *(double2*)&out[(32 * h + row) * RP + col] = *(const double2*)&S[row][col];
+      }
+      __syncthreads();
     }
-    __syncthreads();
-  }
   }
 }
 
@@ -644,8 +644,7 @@ __global__ __launch_bounds__(64) void gram_partials(const float* __restrict__ Y,
 }
 
 // two independent Gram partials in one launch (Bp Bp^T and Q^T Q before the gate):
-// grid (2 GRAM_CHUNKS, batch)
-// S1, S2 = gram_stage(rows1), gram_stage(rows2)
+// grid (2 GRAM_CHUNKS, batch); S1, S2 = gram_stage(rows1), gram_stage(rows2)
 template <bool S1, bool S2>
 __global__ __launch_bounds__(64) void gram_partials_pair(const float* __restrict__ Y1, int rows1,
                                                          double* __restrict__ part1,
